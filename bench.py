@@ -1,0 +1,205 @@
+"""Decode throughput of the whisper decoder token loop on one MI355X.
+
+Default workload: large-v3 decoder (d=1280, 32 layers, 20 heads, V=51866,
+n_text_ctx 448), seeded N(0,0.02) weights quantised to Q8_0 with the
+cmd/quantize rule, synthetic 1500x1280 N(0,1) encoder output, greedy decoding
+at batch 1 from the SOT/en/transcribe prompt. A step is one decoded token
+(forward + repetition penalty + argmax on device; only the id crosses PCIe).
+`--warmup` steps (the first includes nothing extra: the cross K/V are built
+when the sequence is created) run untimed, then `--steps` steps are timed.
+
+Also reported:
+* roofline: the dominant kernel class measured with HIP events around every
+  launch in a separate profiled pass of the same steps; achieved = algorithmic
+  bytes / kernel time, against 8 TB/s.
+* cpu_baseline: the oracle (a C restatement of the Go decoder) on the host
+  cores, one thread (the reference's batch-1 GEMV is single-threaded), on a
+  bounded sample of the same workload.
+
+`--gemv` instead runs the standalone quantised-GEMV microbench (rows x cols at
+batch 1 and 5 for each format, rotating over >= 1 GiB of distinct copies).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+import __graft_entry__  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+QNAMES = {"Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q8_0": 8}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(wh, tensors, meta, enc, prompt, n_tokens, gpu_tokens):
+    from oracle import oracle as orc  # the checker, timed as the CPU baseline
+
+    threads = min(16, os.cpu_count() or 1)
+    t0 = time.time()
+    ref = orc.OracleModel(tensors, meta, dot_variant=1, threads=threads)
+    st = ref.state(prompt)
+    st.prepare_cross(enc)  # the one-time cross K/V precompute, multi-threaded, untimed
+    t_cross = time.time() - t0
+    toks = list(prompt)
+    t1 = time.perf_counter()
+    for _ in range(n_tokens):
+        logits = st.forward(enc)
+        cur = orc.repetition_penalty(logits, np.array(toks, np.int32))
+        nxt = orc.sample_greedy(cur, 1.0, eot=50256)
+        toks.append(int(nxt))
+        st.push(nxt)
+    dt = time.perf_counter() - t1
+    gen = toks[len(prompt):]
+    return {"value": n_tokens / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{n_tokens} greedy steps of the same workload after the cross K/V precompute "
+                      f"({t_cross:.1f}s on {threads} threads, untimed)",
+            "tokens_match_gpu": gen == gpu_tokens[:len(gen)]}
+
+
+def run_decode(args):
+    wh = __graft_entry__.load_package()
+    if wh.native.device_count() < 1:
+        raise SystemExit("bench: no GPU visible")
+    qtype = QNAMES[args.qtype]
+    t0 = time.time()
+    tensors, meta = wh.synth.make_decoder(args.config, qtype)
+    d = meta["n_state"]
+    enc = wh.synth.encoder_output(args.config, d, stream=0)
+    prompt = list(wh.synth.SOT_EN_TRANSCRIBE)
+    wbytes = wh.synth.weight_bytes_per_token(tensors)
+    log(f"bench: model {args.config} {args.qtype} generated in {time.time() - t0:.1f}s, {wbytes} weight B/token")
+    t0 = time.time()
+    dec = wh.HIPDecoder(tensors, meta, device=0)
+    seq = dec.sequence([enc])
+    seq.set_tokens(0, prompt)
+    log(f"bench: uploaded + cross K/V in {time.time() - t0:.2f}s")
+    total = args.warmup + args.steps + args.profile_steps
+    if len(prompt) + total > meta["n_ctx"]:
+        raise SystemExit(f"bench: {total} steps exceed n_text_ctx {meta['n_ctx']}")
+    tokens = []
+    for _ in range(args.warmup):
+        tokens.append(seq.step_greedy()[0])
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        tokens.append(seq.step_greedy()[0])
+    dt = time.perf_counter() - t1
+    log(f"bench: {args.steps} steps in {dt * 1e3:.1f} ms")
+    # profiled pass: event pair around every launch
+    seq.set_profiling(True)
+    for _ in range(args.profile_steps):
+        tokens.append(seq.step_greedy()[0])
+    prof = seq.profile()
+    seq.set_profiling(False)
+    stop = None
+    for i, t in enumerate(tokens):
+        if t == dec.eot:
+            stop = i + 1
+            break
+    kern_ms = {k: v[0] for k, v in prof.items()}
+    dom = max(kern_ms, key=kern_ms.get)
+    dms, dcount, dbytes = prof[dom]
+    achieved = dbytes / (dms * 1e-3) / 1e9 if dms > 0 else 0.0
+    value = args.steps / dt
+    out = {
+        "metric": "decode tokens/s (large-v3 Q8_0, bs=1)" if args.config == "large-v3" and args.qtype == "Q8_0"
+        else f"decode tokens/s ({args.config} {args.qtype}, bs=1)",
+        "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32 activations, " + args.qtype + " weights", "data": "synthetic",
+        "config": {"workload": f"whisper {args.config} decoder, {args.qtype}, greedy, batch 1, "
+                               f"1500x{d} synthetic encoder output", "global_batch": 1,
+                   "prompt": prompt, "steps_timed": args.steps},
+        "weight_bytes_per_token": wbytes,
+        "weight_roofline_frac": round(wbytes * value / (HBM_PEAK_GBS * 1e9), 4),
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "launches": dcount, "avg_launch_us": round(dms * 1e3 / max(dcount, 1), 3),
+                     "bytes_per_launch": round(dbytes / max(dcount, 1)), "traffic": None},
+        "kernel_ms_per_step": {k: round(v / args.profile_steps, 4) for k, v in kern_ms.items()},
+        "stopped_at_step": stop,
+    }
+    seq.close()
+    dec.close()
+    if args.cpu_tokens > 0:
+        log("bench: cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline(wh, tensors, meta, enc, prompt, args.cpu_tokens, tokens)
+    print(json.dumps(out), flush=True)
+
+
+def run_gemv(args):
+    """Standalone quantised GEMV at the large-v3 decoder shapes."""
+    import ctypes as C
+
+    wh = __graft_entry__.load_package()
+    lib = wh.native.lib()
+    shapes = [(1280, 1280), (5120, 1280), (1280, 5120), (51866, 1280)]
+    fmts = args.gemv_formats.split(",")
+    st = wh.native.Stream()
+    e0, e1 = wh.native.Event(), wh.native.Event()
+    rows_out = []
+    for fmt in fmts:
+        qt = QNAMES[fmt]
+        for rows, cols in shapes:
+            rng = np.random.default_rng(rows + cols)
+            w = (rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02))
+            raw = wh.quant.quantize(qt, w)
+            nbytes = raw.size
+            ncopy = max(2, min(256, int(np.ceil((1 << 30) / nbytes))))
+            mats = []
+            for _ in range(ncopy):
+                h = C.c_void_p()
+                wh.native.check(lib.wh_matrix_create(qt, rows, cols, raw.ctypes.data, raw.size, 0, C.byref(h)))
+                mats.append(h)
+            for batch in (1, 5):
+                x = wh.native.DevBuf.from_array(rng.standard_normal((batch, cols)).astype(np.float32))
+                y = wh.native.DevBuf(batch * rows * 4)
+                for h in mats[:4]:
+                    wh.native.check(lib.wh_gemv(h, x.ptr, batch, y.ptr, st.h))
+                iters = max(100, ncopy)
+                e0.record(st)
+                for i in range(iters):
+                    lib.wh_gemv(mats[i % ncopy], x.ptr, batch, y.ptr, st.h)
+                e1.record(st)
+                ms = e0.elapsed_ms(e1) / iters
+                gbs = nbytes / (ms * 1e-3) / 1e9
+                rows_out.append({"format": fmt, "rows": rows, "cols": cols, "batch": batch, "bytes": nbytes,
+                                 "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                                 "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": ncopy})
+                log(json.dumps(rows_out[-1]))
+            for h in mats:
+                lib.wh_matrix_destroy(h)
+    print(json.dumps({"metric": "quant-GEMV HBM GB/s as % of peak", "rows": rows_out}), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=216)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--config", default="large-v3")
+    ap.add_argument("--qtype", default="Q8_0", choices=sorted(QNAMES))
+    ap.add_argument("--profile-steps", type=int, default=16)
+    ap.add_argument("--cpu-tokens", type=int, default=3, help="oracle steps timed for cpu_baseline (0 = skip)")
+    ap.add_argument("--gemv", action="store_true", help="run the standalone GEMV microbench instead")
+    ap.add_argument("--gemv-formats", default="Q8_0,Q4_0,Q4_1,Q5_0,Q5_1")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(streams shard data-parallel across GPUs with no collective; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    if args.gemv:
+        run_gemv(args)
+    else:
+        run_decode(args)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,146 @@
+// Internal declarations shared by the host (.cpp) and device (.hip) sources of
+// libwhisper_hip.so. Not part of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../include/whisper_hip.h"
+
+namespace wh {
+
+// ---- errors -----------------------------------------------------------------
+void set_error(const std::string &msg);
+int fail(int code, const std::string &msg);
+#define WH_HIP(call)                                                                         \
+    do {                                                                                     \
+        hipError_t e_ = (call);                                                              \
+        if (e_ != hipSuccess)                                                                \
+            return ::wh::fail(WH_ERR_HIP, std::string("hip: ") + #call + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+// ---- device matrix layout ------------------------------------------------------
+// A GGUF-block matrix [rows, cols] re-laid out for coalesced 128-bit streaming:
+// quants and per-block scale words live in separate row-major planes so every
+// lane's block payload is 16-byte aligned. Values are bit-identical to the
+// GGUF blocks (the same f16 words, nibbles and high bits).
+//   F32 (F16 is widened to F32 exactly at upload):  f32  [rows][nb*32]
+//   Q8_0: qs int8 [rows][nb*32]   sc f16   [rows][nb]
+//   Q4_0: qs u8   [rows][nb*16]   sc f16   [rows][nb]
+//   Q4_1: qs u8   [rows][nb*16]   sc f16x2 [rows][nb]  (d low, m high)
+//   Q5_0: qs u8   [rows][nb*16]   qh u32   [rows][nb]   sc f16   [rows][nb]
+//   Q5_1: qs u8   [rows][nb*16]   qh u32   [rows][nb]   sc f16x2 [rows][nb]
+// Padding of the tail block (cols % 32 != 0) is whatever the GGUF tail block
+// holds; kernels mask x beyond cols.
+struct DevMat {
+    uint32_t type = 0;
+    int32_t rows = 0, cols = 0, nb = 0;
+    void *qs = nullptr;       // quants (or f32 data)
+    void *sc = nullptr;       // scale words (uint16 or uint32)
+    uint32_t *qh = nullptr;   // Q5 high bits
+    void *alloc = nullptr;    // single device allocation holding all planes
+    uint64_t algo_bytes = 0;  // GGUF bytes (rows * row_bytes)
+    uint64_t dev_bytes = 0;
+};
+
+uint64_t gguf_row_bytes(uint32_t type, uint64_t n);
+bool is_quant_type(uint32_t type);
+uint16_t f32_to_f16(float f);
+float f16_to_f32(uint16_t h);
+int quantize(uint32_t type, const float *src, uint64_t n, uint8_t *dst, uint64_t dst_bytes, int threads);
+int should_quantize(const char *name);
+// Host dequantisation of raw GGUF data (internal/gguf/dequant.go:47-201).
+int dequantize_host(uint32_t type, const uint8_t *raw, uint64_t n, float *out);
+// Size the device planes for a [rows, cols] matrix of `type`, then scatter the
+// raw GGUF rows (of src_type) into them and upload.
+int devmat_plan(DevMat &m, uint32_t type, int32_t rows, int32_t cols);
+int devmat_upload_typed(DevMat &m, uint32_t src_type, const uint8_t *raw, uint64_t nbytes);
+void devmat_free(DevMat &m);
+
+// ---- model ------------------------------------------------------------------------
+struct Layer {
+    float *ln1w, *ln1b, *sqb, *svb, *sob, *ln2w, *ln2b, *cqb, *cvb, *cob, *ln3w, *ln3b, *fc1b, *fc2b;
+    DevMat sq, sk, sv, so, cq, ck, cv, co, fc1, fc2;
+};
+
+}  // namespace wh
+
+struct wh_model {
+    int32_t device = 0;
+    int32_t n_vocab = 0, n_state = 0, n_head = 0, n_layer = 0, n_ctx = 0;
+    int32_t eot = 50256;
+    int32_t attn_mode = 0;  // 0 reference-compatible, 1 textbook causal
+    wh::DevMat tok;         // token embedding [n_vocab, n_state] (tied logits matrix)
+    float *pos = nullptr;   // positional embedding [n_ctx, n_state]
+    float *lnw = nullptr, *lnb = nullptr;
+    std::vector<wh::Layer> layers;
+    void *vec_alloc = nullptr;  // one allocation for every float vector
+    uint64_t weight_bytes = 0;
+};
+
+struct wh_matrix {
+    wh::DevMat m;
+    int32_t device = 0;
+};
+
+namespace wh {
+
+// ---- kernel launchers (wh_kernels.hip) --------------------------------------------
+struct GemvOut {
+    float *y = nullptr;        // [batch, ldy]
+    int32_t ldy = 0;
+    const float *bias = nullptr;
+    const float *res = nullptr;  // y = res + (dot + bias)  (res may alias y)
+    int32_t ldres = 0;
+    int32_t gelu = 0;            // y = gelu(dot + bias)
+};
+struct GemvIn {
+    const float *x = nullptr;  // [batch, ldx]
+    int32_t ldx = 0;
+};
+// Up to 3 matrices of the same type in one launch (e.g. q,k,v).
+int launch_gemv(const DevMat *const *mats, const GemvIn *in, const GemvOut *out, int nmat, int batch,
+                hipStream_t st);
+int launch_dequant_rows(const DevMat &m, int32_t row0, int32_t nrows, float *out, hipStream_t st);
+
+struct SeqDev;  // defined in wh_seq.cpp
+int launch_embed(const wh_model &m, const int32_t *tok, const int32_t *pos, const int32_t *active, float *x,
+                 int S, hipStream_t st);
+int launch_layernorm(const float *x, const float *w, const float *b, float *y, int S, int d, hipStream_t st);
+int launch_self_attn(const float *q, const float *k, const float *v, float *kv_layer, size_t kv_stream_stride,
+                     const int32_t *pos, const int32_t *active, float *out, int S, int H, int hd, int ctx,
+                     int mode, hipStream_t st);
+struct CrossBufs {
+    float *scores;     // [S][H][enc_len]
+    float *cmax;       // [S][H][C]
+    float *psum;       // [S][H][C]
+    float *pv;         // [S][H][C][hd]
+    int chunks;
+    int chunk_len;
+};
+int launch_cross_attn(const float *q, const float *const *kbase, const float *const *vbase, const int32_t *active,
+                      float *out, int S, int H, int hd, int enc_len, const CrossBufs &b, hipStream_t st);
+int launch_cross_gemm(const DevMat &w, const float *enc, int enc_len, const float *bias, float *out,
+                      hipStream_t st);
+struct SampleBufs {
+    float *cur;          // [S][V] penalised logits
+    float *part_val;     // [S][P]
+    int32_t *part_idx;   // [S][P]
+    float *part_val2;    // [S][P] best excluding eot
+    int32_t *part_idx2;
+    int parts;
+};
+int launch_penalty_argmax(const float *logits, const int32_t *hist, const int32_t *hist_len, int hist_cap,
+                          const int32_t *active, int S, int V, float inv_temp, int eot, const SampleBufs &b,
+                          hipStream_t st);
+int launch_argmax_final(const SampleBufs &b, const float *cur, int S, int V, int eot, int suppress_nst,
+                        float no_speech_thold, const int32_t *active, int32_t *hist, int32_t *hist_len,
+                        int hist_cap, int32_t *tok, int32_t *pos, int32_t *out_ids, hipStream_t st);
+int launch_topk(const float *cur, const int32_t *active, int S, int V, int k, float inv_temp, int32_t *out_tok,
+                float *out_lp, float *out_logz, hipStream_t st);
+
+}  // namespace wh

@@ -1,0 +1,860 @@
+// gfx950 kernels for the whisper.go decoder token loop (multi-kernel path).
+//
+// Each kernel cites the reference function whose arithmetic it carries out
+// (paths relative to the reference repository). Accumulation is fp32; the
+// summation order differs from the Go code's sequential sums (parity is
+// tolerance-based there), except where noted as bit-exact.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+
+#include "wh_device.h"
+#include "wh_internal.h"
+
+namespace wh {
+
+// ---------------------------------------------------------------------------
+// Quantised GEMV: y[m, r] = sum_c x[m, c] * W[r, c]
+// (internal/ml/matmul_q8.go:93-139 with the per-block dot kernels :237-429).
+// A group of LG lanes owns one row; lane g of the group walks blocks
+// g, g+LG, ... so a wavefront streams 64 consecutive 32-weight blocks per
+// step with 16-byte loads. Per block the integer codes are formed exactly,
+// s = sum q_i x_i is accumulated in fp32 and scaled once by d (plus m*sum x
+// for the _1 formats), as the reference AVX2 kernels do
+// (internal/ml/matmul_q8_kernels_amd64.go:15-224).
+// ---------------------------------------------------------------------------
+struct GemvOpDev {
+    const uint8_t *qs;
+    const void *sc;
+    const uint32_t *qh;
+    int32_t rows, cols, nb;
+    const float *x;
+    int32_t ldx;
+    float *y;
+    int32_t ldy;
+    const float *bias;
+    const float *res;
+    int32_t ldres;
+    int32_t gelu;
+    int32_t row_begin;
+};
+struct GemvArgs {
+    GemvOpDev op[3];
+    int32_t nop, batch, total_rows;
+};
+
+// Decode block `blk` of a row into integer-valued floats q[32] and return the
+// scale d (and, for _1 formats, m).
+template <int TYPE>
+__device__ __forceinline__ void load_block(const GemvOpDev &op, size_t blk, float q[32], float &d, float &mm) {
+    mm = 0.0f;
+    if constexpr (TYPE == 0) {
+        const float4 *p = (const float4 *)((const float *)op.qs + blk * 32);
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            float4 v = p[t];
+            q[4 * t] = v.x; q[4 * t + 1] = v.y; q[4 * t + 2] = v.z; q[4 * t + 3] = v.w;
+        }
+        d = 1.0f;
+    } else if constexpr (TYPE == 8) {
+        const uint4 *p = (const uint4 *)(op.qs + blk * 32);
+        uint4 a = p[0], b = p[1];
+        uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            int v = (int)w[t];
+            q[4 * t + 0] = (float)((v << 24) >> 24);
+            q[4 * t + 1] = (float)((v << 16) >> 24);
+            q[4 * t + 2] = (float)((v << 8) >> 24);
+            q[4 * t + 3] = (float)(v >> 24);
+        }
+        d = h2f(((const uint16_t *)op.sc)[blk]);
+    } else {
+        uint4 a = *(const uint4 *)(op.qs + blk * 16);
+        uint32_t w[4] = {a.x, a.y, a.z, a.w};
+        uint32_t hbits = 0;
+        if constexpr (TYPE == 6 || TYPE == 7) hbits = op.qh[blk];
+        const float off = (TYPE == 2) ? 8.0f : (TYPE == 6 ? 16.0f : 0.0f);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                uint32_t byte = (w[t] >> (8 * k)) & 0xFFu;
+                uint32_t lo = byte & 0xFu, hi = byte >> 4;
+                int e0 = 8 * t + 2 * k, e1 = e0 + 1;
+                if constexpr (TYPE == 6 || TYPE == 7) {
+                    lo |= ((hbits >> e0) & 1u) << 4;
+                    hi |= ((hbits >> e1) & 1u) << 4;
+                }
+                q[e0] = (float)lo - off;
+                q[e1] = (float)hi - off;
+            }
+        }
+        if constexpr (TYPE == 3 || TYPE == 7) {
+            uint32_t s = ((const uint32_t *)op.sc)[blk];
+            d = h2f(s & 0xFFFFu);
+            mm = h2f(s >> 16);
+        } else {
+            d = h2f(((const uint16_t *)op.sc)[blk]);
+        }
+    }
+}
+
+template <int TYPE, int LG, int MAXB, bool SAFE>
+__global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
+    constexpr int GPW = 64 / LG;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int gl = lane % LG;
+    const int grow = (blockIdx.x * 4 + wave) * GPW + lane / LG;
+    if (grow >= a.total_rows) return;
+    int oi = 0;
+    if (a.nop > 1 && grow >= a.op[1].row_begin) oi = 1;
+    if (a.nop > 2 && grow >= a.op[2].row_begin) oi = 2;
+    const GemvOpDev &op = a.op[oi];
+    const int r = grow - op.row_begin;
+    const int batch = a.batch;
+
+    float acc[MAXB];
+#pragma unroll
+    for (int m = 0; m < MAXB; m++) acc[m] = 0.0f;
+
+    for (int b = gl; b < op.nb; b += LG) {
+        float q[32], d, mm;
+        size_t blk = (size_t)r * op.nb + b;
+        load_block<TYPE>(op, blk, q, d, mm);
+        const int c0 = b * 32;
+#pragma unroll
+        for (int m = 0; m < MAXB; m++) {
+            if (m < batch) {
+                const float *xp = op.x + (size_t)m * op.ldx + c0;
+                float s = 0.0f, sx = 0.0f;
+                if (!SAFE) {
+                    const float4 *x4 = (const float4 *)xp;
+#pragma unroll
+                    for (int t = 0; t < 8; t++) {
+                        float4 v = x4[t];
+                        s += q[4 * t] * v.x + q[4 * t + 1] * v.y + q[4 * t + 2] * v.z + q[4 * t + 3] * v.w;
+                        if constexpr (TYPE == 3 || TYPE == 7) sx += (v.x + v.y) + (v.z + v.w);
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 32; i++) {
+                        float v = (c0 + i < op.cols) ? xp[i] : 0.0f;
+                        s += q[i] * v;
+                        if constexpr (TYPE == 3 || TYPE == 7) sx += v;
+                    }
+                }
+                if constexpr (TYPE == 3 || TYPE == 7) acc[m] += d * s + mm * sx;
+                else acc[m] += d * s;
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MAXB; m++) acc[m] = group_sum<LG>(acc[m]);
+
+    // epilogue: lane m of the group writes batch row m
+    for (int m = gl; m < batch && m < MAXB; m += LG) {
+        float v = 0.0f;
+#pragma unroll
+        for (int j = 0; j < MAXB; j++)
+            if (j == m) v = acc[j];
+        if (op.bias) v = v + op.bias[r];
+        if (op.gelu) v = gelu_ref(v);
+        if (op.res) v = op.res[(size_t)m * op.ldres + r] + v;
+        op.y[(size_t)m * op.ldy + r] = v;
+    }
+}
+
+template <int TYPE, int LG, int MAXB>
+static void gemv_launch_t(const GemvArgs &a, bool safe, hipStream_t st) {
+    constexpr int rows_per_block = 4 * (64 / LG);
+    dim3 grid((a.total_rows + rows_per_block - 1) / rows_per_block);
+    if (safe) hipLaunchKernelGGL((k_gemv<TYPE, LG, MAXB, true>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_gemv<TYPE, LG, MAXB, false>), grid, dim3(256), 0, st, a);
+}
+
+template <int TYPE>
+static void gemv_launch_type(const GemvArgs &a, int nb, bool safe, hipStream_t st) {
+    const int b = a.batch;
+    if (nb <= 16) {
+        if (b <= 1) gemv_launch_t<TYPE, 16, 1>(a, safe, st);
+        else if (b <= 8) gemv_launch_t<TYPE, 16, 8>(a, safe, st);
+        else gemv_launch_t<TYPE, 16, 16>(a, safe, st);
+    } else {
+        if (b <= 1) gemv_launch_t<TYPE, 64, 1>(a, safe, st);
+        else if (b <= 8) gemv_launch_t<TYPE, 64, 8>(a, safe, st);
+        else gemv_launch_t<TYPE, 64, 16>(a, safe, st);
+    }
+}
+
+int launch_gemv(const DevMat *const *mats, const GemvIn *in, const GemvOut *out, int nmat, int batch,
+                hipStream_t st) {
+    if (nmat < 1 || nmat > 3) return fail(WH_ERR_INVALID, "gemv: 1..3 matrices per launch");
+    if (batch < 1 || batch > 16) return fail(WH_ERR_INVALID, "gemv: batch must be in [1,16]");
+    GemvArgs a;
+    memset(&a, 0, sizeof a);
+    a.nop = nmat;
+    a.batch = batch;
+    int total = 0, nbmax = 0;
+    bool safe = false;
+    const uint32_t type = mats[0]->type;
+    for (int i = 0; i < nmat; i++) {
+        const DevMat &m = *mats[i];
+        if (m.type != type) return fail(WH_ERR_INVALID, "gemv: mixed matrix types in one launch");
+        GemvOpDev &o = a.op[i];
+        o.qs = (const uint8_t *)m.qs;
+        o.sc = m.sc;
+        o.qh = m.qh;
+        o.rows = m.rows;
+        o.cols = m.cols;
+        o.nb = m.nb;
+        o.x = in[i].x;
+        o.ldx = in[i].ldx;
+        o.y = out[i].y;
+        o.ldy = out[i].ldy;
+        o.bias = out[i].bias;
+        o.res = out[i].res;
+        o.ldres = out[i].ldres;
+        o.gelu = out[i].gelu;
+        o.row_begin = total;
+        total += m.rows;
+        if (m.nb > nbmax) nbmax = m.nb;
+        if ((m.cols % 32) != 0 || (in[i].ldx % 4) != 0 || (((uintptr_t)in[i].x) & 15) != 0) safe = true;
+    }
+    a.total_rows = total;
+    switch (type) {
+    case 0: gemv_launch_type<0>(a, nbmax, safe, st); break;
+    case 2: gemv_launch_type<2>(a, nbmax, safe, st); break;
+    case 3: gemv_launch_type<3>(a, nbmax, safe, st); break;
+    case 6: gemv_launch_type<6>(a, nbmax, safe, st); break;
+    case 7: gemv_launch_type<7>(a, nbmax, safe, st); break;
+    case 8: gemv_launch_type<8>(a, nbmax, safe, st); break;
+    default: return fail(WH_ERR_UNSUPPORTED, "gemv: unsupported matrix type");
+    }
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Bit-exact row dequantisation (internal/gguf/dequant.go:47-201).
+// ---------------------------------------------------------------------------
+template <int TYPE>
+__global__ void k_dequant_rows(MatView m, int32_t row0, int32_t nrows, float *out) {
+    size_t n = (size_t)nrows * m.cols;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        int r = row0 + (int)(i / m.cols);
+        int c = (int)(i % m.cols);
+        out[i] = dequant_elem<TYPE>(m, r, c >> 5, c & 31);
+    }
+}
+
+static MatView view_of(const DevMat &d) {
+    MatView v;
+    v.qs = (const uint8_t *)d.qs;
+    v.sc = d.sc;
+    v.qh = d.qh;
+    v.rows = d.rows;
+    v.cols = d.cols;
+    v.nb = d.nb;
+    return v;
+}
+
+int launch_dequant_rows(const DevMat &m, int32_t row0, int32_t nrows, float *out, hipStream_t st) {
+    MatView v = view_of(m);
+    size_t n = (size_t)nrows * m.cols;
+    int grid = (int)((n + 255) / 256);
+    if (grid > 65535) grid = 65535;
+    if (grid < 1) grid = 1;
+    switch (m.type) {
+    case 0: hipLaunchKernelGGL(k_dequant_rows<0>, dim3(grid), dim3(256), 0, st, v, row0, nrows, out); break;
+    case 2: hipLaunchKernelGGL(k_dequant_rows<2>, dim3(grid), dim3(256), 0, st, v, row0, nrows, out); break;
+    case 3: hipLaunchKernelGGL(k_dequant_rows<3>, dim3(grid), dim3(256), 0, st, v, row0, nrows, out); break;
+    case 6: hipLaunchKernelGGL(k_dequant_rows<6>, dim3(grid), dim3(256), 0, st, v, row0, nrows, out); break;
+    case 7: hipLaunchKernelGGL(k_dequant_rows<7>, dim3(grid), dim3(256), 0, st, v, row0, nrows, out); break;
+    case 8: hipLaunchKernelGGL(k_dequant_rows<8>, dim3(grid), dim3(256), 0, st, v, row0, nrows, out); break;
+    default: return fail(WH_ERR_UNSUPPORTED, "dequant: unsupported type");
+    }
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Token + positional embedding (internal/model/decoder.go:756-773). A
+// quantised token embedding row is dequantised bit-exactly (the documented
+// extension for P4: the reference reads an empty float table there).
+// ---------------------------------------------------------------------------
+template <int TYPE>
+__global__ void k_embed(MatView tok, const float *pos_emb, const int32_t *tokv, const int32_t *posv,
+                        const int32_t *active, float *x, int d) {
+    int s = blockIdx.x;
+    if (active && !active[s]) return;
+    int id = tokv[s], p = posv[s];
+    for (int i = threadIdx.x; i < d; i += blockDim.x) {
+        float e = dequant_elem<TYPE>(tok, id, i >> 5, i & 31);
+        x[(size_t)s * d + i] = e + pos_emb[(size_t)p * d + i];
+    }
+}
+
+int launch_embed(const wh_model &m, const int32_t *tok, const int32_t *pos, const int32_t *active, float *x,
+                 int S, hipStream_t st) {
+    MatView v = view_of(m.tok);
+    int d = m.n_state;
+    switch (m.tok.type) {
+    case 0: hipLaunchKernelGGL(k_embed<0>, dim3(S), dim3(256), 0, st, v, m.pos, tok, pos, active, x, d); break;
+    case 2: hipLaunchKernelGGL(k_embed<2>, dim3(S), dim3(256), 0, st, v, m.pos, tok, pos, active, x, d); break;
+    case 3: hipLaunchKernelGGL(k_embed<3>, dim3(S), dim3(256), 0, st, v, m.pos, tok, pos, active, x, d); break;
+    case 6: hipLaunchKernelGGL(k_embed<6>, dim3(S), dim3(256), 0, st, v, m.pos, tok, pos, active, x, d); break;
+    case 7: hipLaunchKernelGGL(k_embed<7>, dim3(S), dim3(256), 0, st, v, m.pos, tok, pos, active, x, d); break;
+    case 8: hipLaunchKernelGGL(k_embed<8>, dim3(S), dim3(256), 0, st, v, m.pos, tok, pos, active, x, d); break;
+    default: return fail(WH_ERR_UNSUPPORTED, "embed: unsupported type");
+    }
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm over d (internal/ml/ops.go:153-202): y = w*(x-mean)/std + b with
+// std = float32(sqrt(float64(var+eps))), eps = 1e-5. One block per row.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float block_sum256(float v, float *red) {
+    v = group_sum<64>(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.0f;
+    const int nw = blockDim.x >> 6;
+    for (int i = 0; i < nw; i++) t += red[i];
+    return t;
+}
+
+__global__ __launch_bounds__(256) void k_layernorm(const float *x, const float *w, const float *b, float *y,
+                                                   int d) {
+    __shared__ float red[8];
+    const float *xr = x + (size_t)blockIdx.x * d;
+    float *yr = y + (size_t)blockIdx.x * d;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) s += xr[i];
+    float mean = block_sum256(s, red) / (float)d;
+    float v = 0.0f;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) {
+        float t = xr[i] - mean;
+        v += t * t;
+    }
+    float var = block_sum256(v, red) / (float)d;
+    float sd = (float)sqrt((double)(var + 1e-5f));
+    __syncthreads();
+    for (int i = threadIdx.x; i < d; i += blockDim.x) yr[i] = w[i] * (xr[i] - mean) / sd + b[i];
+}
+
+int launch_layernorm(const float *x, const float *w, const float *b, float *y, int S, int d, hipStream_t st) {
+    hipLaunchKernelGGL(k_layernorm, dim3(S), dim3(256), 0, st, x, w, b, y, d);
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Decoder self-attention with the persistent KV cache
+// (internal/model/decoder.go:836-908 + internal/ml/attention.go:193-281).
+// KV layout per stream and layer: [2][H][ctx][hd] (K plane, then V plane).
+// mode 0 reproduces the reference mask: with Tq = 1 every key j > 0 is masked
+// (attention.go:250-256), so only cache row 0 is attended. mode 1 attends to
+// rows 0..pos (textbook causal decoding). One wavefront per (stream, head).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void k_self_attn(const float *q, const float *k, const float *v, float *kv_layer,
+                                                  size_t kv_stream_stride, const int32_t *posv,
+                                                  const int32_t *active, float *out, int H, int hd, int ctx,
+                                                  int mode, float scale) {
+    extern __shared__ float sc[];
+    const int s = blockIdx.x / H, h = blockIdx.x % H, lane = threadIdx.x;
+    if (active && !active[s]) return;
+    const int d = H * hd;
+    const int p = posv[s];
+    float *Kc = kv_layer + (size_t)s * kv_stream_stride + (size_t)h * ctx * hd;
+    float *Vc = Kc + (size_t)H * ctx * hd;
+    const float *qh = q + (size_t)s * d + (size_t)h * hd;
+    const float *kh = k + (size_t)s * d + (size_t)h * hd;
+    const float *vh = v + (size_t)s * d + (size_t)h * hd;
+    for (int j = lane; j < hd; j += 64) {
+        Kc[(size_t)p * hd + j] = kh[j];
+        Vc[(size_t)p * hd + j] = vh[j];
+    }
+    const int n = (mode == 0) ? 1 : p + 1;
+    float mx = -INFINITY;
+    for (int t = 0; t < n; t++) {
+        const float *kr = (t == p) ? kh : Kc + (size_t)t * hd;
+        float part = 0.0f;
+        for (int j = lane; j < hd; j += 64) part += qh[j] * kr[j];
+        float sco = group_sum<64>(part) * scale;
+        if (lane == 0) sc[t] = sco;
+        mx = fmaxf(mx, sco);
+    }
+    __syncthreads();
+    float sum = 0.0f;
+    for (int t = lane; t < n; t += 64) {
+        float e = fast_exp(sc[t] - mx);
+        sc[t] = e;
+        sum += e;
+    }
+    sum = group_sum<64>(sum);
+    __syncthreads();
+    const bool uniform = (sum == 0.0f);
+    const float inv = uniform ? 1.0f / (float)n : 1.0f / sum;
+    for (int j = lane; j < hd; j += 64) {
+        float o = 0.0f;
+        for (int t = 0; t < n; t++) {
+            const float *vr = (t == p) ? vh : Vc + (size_t)t * hd;
+            float pt = uniform ? inv : sc[t] * inv;
+            o += pt * vr[j];
+        }
+        out[(size_t)s * d + (size_t)h * hd + j] = o;
+    }
+}
+
+int launch_self_attn(const float *q, const float *k, const float *v, float *kv_layer, size_t kv_stream_stride,
+                     const int32_t *pos, const int32_t *active, float *out, int S, int H, int hd, int ctx, int mode,
+                     hipStream_t st) {
+    float scale = (float)(1.0 / sqrt((double)hd));
+    size_t shmem = sizeof(float) * (size_t)(mode == 0 ? 1 : ctx);
+    hipLaunchKernelGGL(k_self_attn, dim3(S * H), dim3(64), shmem, st, q, k, v, kv_layer, kv_stream_stride, pos,
+                       active, out, H, hd, ctx, mode, scale);
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Cross-attention over the cached encoder K/V
+// (internal/model/decoder.go:911-971, P3 addressing :949-951): the [enc_len, d]
+// row-major projection is viewed as [H, enc_len, hd] without a transpose, so
+// head h reads the contiguous slab [h*enc_len*hd, (h+1)*enc_len*hd).
+// hd == 64: split over key chunks in three kernels; the softmax subtracts the
+// exact global maximum before the fast exp, as the reference does
+// (attention.go:93-131). Other head sizes: one block per (stream, head).
+// ---------------------------------------------------------------------------
+constexpr int CROSS_CHUNK = 128;
+
+__global__ __launch_bounds__(256) void k_cross_scores64(const float *q, const float *const *kbase,
+                                                        const int32_t *active, float *scores, float *cmax, int H,
+                                                        int enc_len, int chunks, float scale) {
+    __shared__ float red[4];
+    const int c = blockIdx.x % chunks, sh = blockIdx.x / chunks, h = sh % H, s = sh / H;
+    if (active && !active[s]) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, slot = lane & 15;
+    const int d = H * 64;
+    const float4 q4 = ((const float4 *)(q + (size_t)s * d + h * 64))[slot];
+    const float *K = kbase[s] + (size_t)h * enc_len * 64;
+    const int t0 = c * CROSS_CHUNK, t1 = min(t0 + CROSS_CHUNK, enc_len);
+    float mx = -INFINITY;
+    for (int t = t0 + wave * 4 + (lane >> 4); t - (lane >> 4) < t1; t += 16) {
+        float part = 0.0f;
+        if (t < t1) {
+            float4 k4 = ((const float4 *)(K + (size_t)t * 64))[slot];
+            part = q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
+        }
+        float dot = group_sum<16>(part);
+        if (t < t1) {
+            float sco = dot * scale;
+            if (slot == 0) scores[((size_t)s * H + h) * enc_len + t] = sco;
+            mx = fmaxf(mx, sco);
+        }
+    }
+    mx = group_max<64>(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0) cmax[((size_t)s * H + h) * chunks + c] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__global__ __launch_bounds__(256) void k_cross_pv64(const float *const *vbase, const int32_t *active,
+                                                    const float *scores, const float *cmax, float *psum, float *pv,
+                                                    int H, int enc_len, int chunks) {
+    __shared__ float4 red4[4][16];
+    __shared__ float reds[4];
+    const int c = blockIdx.x % chunks, sh = blockIdx.x / chunks, h = sh % H, s = sh / H;
+    if (active && !active[s]) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, slot = lane & 15;
+    float M = -INFINITY;
+    const float *cm = cmax + ((size_t)s * H + h) * chunks;
+    for (int i = 0; i < chunks; i++) M = fmaxf(M, cm[i]);
+    const float *V = vbase[s] + (size_t)h * enc_len * 64;
+    const float *sc = scores + ((size_t)s * H + h) * enc_len;
+    const int t0 = c * CROSS_CHUNK, t1 = min(t0 + CROSS_CHUNK, enc_len);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float es = 0.0f;
+    for (int t = t0 + wave * 4 + (lane >> 4); t < t1; t += 16) {
+        float e = fast_exp(sc[t] - M);
+        float4 v4 = ((const float4 *)(V + (size_t)t * 64))[slot];
+        acc.x += e * v4.x; acc.y += e * v4.y; acc.z += e * v4.z; acc.w += e * v4.w;
+        if (slot == 0) es += e;
+    }
+    // reduce the 4 key groups of the wave (lanes differing in bits 4,5)
+#pragma unroll
+    for (int o = 16; o < 64; o <<= 1) {
+        acc.x += __shfl_xor(acc.x, o, 64);
+        acc.y += __shfl_xor(acc.y, o, 64);
+        acc.z += __shfl_xor(acc.z, o, 64);
+        acc.w += __shfl_xor(acc.w, o, 64);
+    }
+    es = group_sum<64>(es);
+    if (lane < 16) red4[wave][lane] = acc;
+    if (lane == 0) reds[wave] = es;
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        float4 r = red4[0][threadIdx.x];
+        for (int w = 1; w < 4; w++) {
+            float4 t = red4[w][threadIdx.x];
+            r.x += t.x; r.y += t.y; r.z += t.z; r.w += t.w;
+        }
+        ((float4 *)(pv + (((size_t)s * H + h) * chunks + c) * 64))[threadIdx.x] = r;
+    }
+    if (threadIdx.x == 0) psum[((size_t)s * H + h) * chunks + c] = (reds[0] + reds[1]) + (reds[2] + reds[3]);
+}
+
+__global__ __launch_bounds__(64) void k_cross_combine64(const int32_t *active, const float *psum, const float *pv,
+                                                        float *out, int H, int chunks) {
+    const int sh = blockIdx.x, h = sh % H, s = sh / H;
+    if (active && !active[s]) return;
+    const float *ps = psum + (size_t)sh * chunks;
+    float sum = 0.0f;
+    for (int i = 0; i < chunks; i++) sum += ps[i];
+    const float inv = 1.0f / sum;  // sum >= 1: the maximum key contributes fast_exp(0) = 1
+    float o = 0.0f;
+    for (int i = 0; i < chunks; i++) o += pv[((size_t)sh * chunks + i) * 64 + threadIdx.x];
+    out[(size_t)s * H * 64 + h * 64 + threadIdx.x] = o * inv;
+}
+
+__global__ __launch_bounds__(256) void k_cross_generic(const float *q, const float *const *kbase,
+                                                       const float *const *vbase, const int32_t *active, float *out,
+                                                       int H, int hd, int enc_len, float scale) {
+    extern __shared__ float sc[];
+    __shared__ float red[8];
+    const int s = blockIdx.x / H, h = blockIdx.x % H;
+    if (active && !active[s]) return;
+    const int d = H * hd;
+    const float *qh = q + (size_t)s * d + (size_t)h * hd;
+    const float *K = kbase[s] + (size_t)h * enc_len * hd;
+    const float *V = vbase[s] + (size_t)h * enc_len * hd;
+    float mx = -INFINITY;
+    for (int t = threadIdx.x; t < enc_len; t += blockDim.x) {
+        float dot = 0.0f;
+        for (int j = 0; j < hd; j++) dot += qh[j] * K[(size_t)t * hd + j];
+        float sco = dot * scale;
+        sc[t] = sco;
+        mx = fmaxf(mx, sco);
+    }
+    mx = group_max<64>(mx);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = red[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); i++) mx = fmaxf(mx, red[i]);
+    __syncthreads();
+    float es = 0.0f;
+    for (int t = threadIdx.x; t < enc_len; t += blockDim.x) {
+        float e = fast_exp(sc[t] - mx);
+        sc[t] = e;
+        es += e;
+    }
+    float sum = block_sum256(es, red);
+    __syncthreads();
+    const float inv = 1.0f / sum;
+    for (int j = threadIdx.x; j < hd; j += blockDim.x) {
+        float o = 0.0f;
+        for (int t = 0; t < enc_len; t++) o += sc[t] * V[(size_t)t * hd + j];
+        out[(size_t)s * d + (size_t)h * hd + j] = o * inv;
+    }
+}
+
+int launch_cross_attn(const float *q, const float *const *kbase, const float *const *vbase, const int32_t *active,
+                      float *out, int S, int H, int hd, int enc_len, const CrossBufs &b, hipStream_t st) {
+    float scale = (float)(1.0 / sqrt((double)hd));
+    if (hd == 64) {
+        int chunks = b.chunks;
+        hipLaunchKernelGGL(k_cross_scores64, dim3(S * H * chunks), dim3(256), 0, st, q, kbase, active, b.scores,
+                           b.cmax, H, enc_len, chunks, scale);
+        hipLaunchKernelGGL(k_cross_pv64, dim3(S * H * chunks), dim3(256), 0, st, vbase, active, b.scores, b.cmax,
+                           b.psum, b.pv, H, enc_len, chunks);
+        hipLaunchKernelGGL(k_cross_combine64, dim3(S * H), dim3(64), 0, st, active, b.psum, b.pv, out, H, chunks);
+    } else {
+        size_t shmem = sizeof(float) * (size_t)enc_len;
+        if (shmem > 64 * 1024) return fail(WH_ERR_UNSUPPORTED, "cross-attention: encoder length too large for head size");
+        hipLaunchKernelGGL(k_cross_generic, dim3(S * H), dim3(256), shmem, st, q, kbase, vbase, active, out, H, hd,
+                           enc_len, scale);
+    }
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Cross K/V projection: C[t, r] = sum_c E[t, c] * W[r, c] (+ bias[r]) for all
+// encoder frames (internal/model/decoder.go:923-940 via
+// internal/ml/matmul_q8.go:141-196). Tiled fp32 GEMM: a 64x64 output tile per
+// block, K-steps of one 32-weight block dequantised bit-exactly into LDS.
+// ---------------------------------------------------------------------------
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_cross_gemm(MatView w, const float *E, int T, const float *bias, float *C) {
+    __shared__ float Es[32][64 + 4];
+    __shared__ float Ws[32][64 + 4];
+    const int t0 = blockIdx.y * 64, r0 = blockIdx.x * 64;
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const int K = w.cols;
+    float acc[4][4] = {};
+    for (int b = 0; b < w.nb; b++) {
+        const int c0 = b * 32;
+        // E tile: 64 frames x 32 columns
+        for (int i = threadIdx.x; i < 64 * 32; i += 256) {
+            int tt = i / 32, cc = i % 32;
+            int t = t0 + tt, c = c0 + cc;
+            Es[cc][tt] = (t < T && c < K) ? E[(size_t)t * K + c] : 0.0f;
+        }
+        for (int i = threadIdx.x; i < 64 * 32; i += 256) {
+            int rr = i / 32, cc = i % 32;
+            int r = r0 + rr;
+            Ws[cc][rr] = (r < w.rows && c0 + cc < K) ? dequant_elem<TYPE>(w, r, b, cc) : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll 8
+        for (int kk = 0; kk < 32; kk++) {
+            float av[4], bv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) av[i] = Es[kk][ty * 4 + i];
+#pragma unroll
+            for (int j = 0; j < 4; j++) bv[j] = Ws[kk][tx * 4 + j];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] += av[i] * bv[j];
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int t = t0 + ty * 4 + i;
+        if (t >= T) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            int r = r0 + tx * 4 + j;
+            if (r < w.rows) C[(size_t)t * w.rows + r] = bias ? acc[i][j] + bias[r] : acc[i][j];
+        }
+    }
+}
+
+int launch_cross_gemm(const DevMat &w, const float *enc, int enc_len, const float *bias, float *out, hipStream_t st) {
+    MatView v = view_of(w);
+    dim3 grid((w.rows + 63) / 64, (enc_len + 63) / 64);
+    switch (w.type) {
+    case 0: hipLaunchKernelGGL(k_cross_gemm<0>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
+    case 2: hipLaunchKernelGGL(k_cross_gemm<2>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
+    case 3: hipLaunchKernelGGL(k_cross_gemm<3>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
+    case 6: hipLaunchKernelGGL(k_cross_gemm<6>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
+    case 7: hipLaunchKernelGGL(k_cross_gemm<7>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
+    case 8: hipLaunchKernelGGL(k_cross_gemm<8>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
+    default: return fail(WH_ERR_UNSUPPORTED, "cross gemm: unsupported type");
+    }
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Repetition penalty + greedy argmax on device
+// (internal/model/decoder.go:1140-1167 and :996-1034). The penalty subtracts
+// 2.0*count over the last 128 history ids (prompt included) from a copy of
+// the logits; selection is the first index of the maximum of logit*invTemp.
+// Stage 1: per-part maxima; stage 2: ordered reduction + SuppressNST + append.
+// ---------------------------------------------------------------------------
+constexpr int PEN_WINDOW = 128;
+
+__device__ __forceinline__ void better(float v, int i, float &bv, int &bi) {
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+
+__global__ __launch_bounds__(256) void k_penalty_argmax(const float *logits, const int32_t *hist,
+                                                        const int32_t *hist_len, int hist_cap, const int32_t *active,
+                                                        int V, float inv_temp, int eot, float *cur, float *pval,
+                                                        int32_t *pidx, float *pval2, int32_t *pidx2, int parts) {
+    __shared__ int32_t win[PEN_WINDOW];
+    __shared__ float rv[4], rv2[4];
+    __shared__ int ri[4], ri2[4];
+    const int s = blockIdx.y, part = blockIdx.x;
+    if (active && !active[s]) return;
+    const int len = hist_len[s];
+    const int start = len > PEN_WINDOW ? len - PEN_WINDOW : 0;
+    const int nwin = len - start;
+    for (int i = threadIdx.x; i < nwin; i += blockDim.x) win[i] = hist[(size_t)s * hist_cap + start + i];
+    __syncthreads();
+    const int per = (V + parts - 1) / parts;
+    const int i0 = part * per, i1 = min(V, i0 + per);
+    float bv = -INFINITY, bv2 = -INFINITY;
+    int bi = 0x7FFFFFFF, bi2 = 0x7FFFFFFF;
+    const float *lg = logits + (size_t)s * V;
+    float *cu = cur + (size_t)s * V;
+    for (int i = i0 + threadIdx.x; i < i1; i += blockDim.x) {
+        int cnt = 0;
+        for (int w = 0; w < nwin; w++) cnt += (win[w] == i);
+        float v = lg[i];
+        if (cnt > 0) v -= 2.0f * (float)cnt;
+        cu[i] = v;
+        float sc = v * inv_temp;
+        better(sc, i, bv, bi);
+        if (i != eot) better(sc, i, bv2, bi2);
+    }
+    // wave reduce (value, index) pairs
+    for (int o = 32; o > 0; o >>= 1) {
+        float ov = __shfl_xor(bv, o, 64);
+        int oi = __shfl_xor(bi, o, 64);
+        better(ov, oi, bv, bi);
+        float ov2 = __shfl_xor(bv2, o, 64);
+        int oi2 = __shfl_xor(bi2, o, 64);
+        better(ov2, oi2, bv2, bi2);
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) { rv[wave] = bv; ri[wave] = bi; rv2[wave] = bv2; ri2[wave] = bi2; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++) { better(rv[w], ri[w], rv[0], ri[0]); better(rv2[w], ri2[w], rv2[0], ri2[0]); }
+        pval[(size_t)s * parts + part] = rv[0];
+        pidx[(size_t)s * parts + part] = ri[0];
+        pval2[(size_t)s * parts + part] = rv2[0];
+        pidx2[(size_t)s * parts + part] = ri2[0];
+    }
+}
+
+__global__ void k_argmax_final(const float *pval, const int32_t *pidx, const float *pval2, const int32_t *pidx2,
+                               int parts, const float *cur, int V, int eot, int suppress_nst, float nst,
+                               const int32_t *active, int32_t *hist, int32_t *hist_len, int hist_cap, int32_t *tok,
+                               int32_t *pos, int32_t *out_ids) {
+    const int s = blockIdx.x;
+    if (threadIdx.x != 0) return;
+    if (active && !active[s]) { if (out_ids) out_ids[s] = -1; return; }
+    float bv = -INFINITY, bv2 = -INFINITY;
+    int bi = 0x7FFFFFFF, bi2 = 0x7FFFFFFF;
+    for (int p = 0; p < parts; p++) {
+        better(pval[(size_t)s * parts + p], pidx[(size_t)s * parts + p], bv, bi);
+        better(pval2[(size_t)s * parts + p], pidx2[(size_t)s * parts + p], bv2, bi2);
+    }
+    if (bi == 0x7FFFFFFF) bi = 0;  // all values NaN: the reference keeps index 0
+    int id = bi;
+    if (suppress_nst && eot >= 0 && eot < V) {
+        if (cur[(size_t)s * V + eot] < -nst && id == eot) id = (bi2 == 0x7FFFFFFF) ? eot : bi2;
+    }
+    int len = hist_len[s];
+    if (len < hist_cap) hist[(size_t)s * hist_cap + len] = id;
+    hist_len[s] = len + 1;
+    tok[s] = id;
+    pos[s] = len;
+    if (out_ids) out_ids[s] = id;
+}
+
+int launch_penalty_argmax(const float *logits, const int32_t *hist, const int32_t *hist_len, int hist_cap,
+                          const int32_t *active, int S, int V, float inv_temp, int eot, const SampleBufs &b,
+                          hipStream_t st) {
+    hipLaunchKernelGGL(k_penalty_argmax, dim3(b.parts, S), dim3(256), 0, st, logits, hist, hist_len, hist_cap,
+                       active, V, inv_temp, eot, b.cur, b.part_val, b.part_idx, b.part_val2, b.part_idx2, b.parts);
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+int launch_argmax_final(const SampleBufs &b, const float *cur, int S, int V, int eot, int suppress_nst,
+                        float no_speech_thold, const int32_t *active, int32_t *hist, int32_t *hist_len, int hist_cap,
+                        int32_t *tok, int32_t *pos, int32_t *out_ids, hipStream_t st) {
+    hipLaunchKernelGGL(k_argmax_final, dim3(S), dim3(64), 0, st, b.part_val, b.part_idx, b.part_val2, b.part_idx2,
+                       b.parts, cur, V, eot, suppress_nst, no_speech_thold, active, hist, hist_len, hist_cap, tok, pos,
+                       out_ids);
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Top-k with log-normaliser for beam search (internal/model/decoder.go:1068-1136):
+// s_i = v_i*invTemp; keep the k largest (value desc, index asc); logZ =
+// log(sum float32(exp(float64(s_i - max)))) + max; logprob = s - logZ.
+// One block per stream.
+// ---------------------------------------------------------------------------
+constexpr int TOPK_MAX = 8;
+
+__global__ __launch_bounds__(256) void k_topk(const float *cur, const int32_t *active, int V, int k, float inv_temp,
+                                              int32_t *out_tok, float *out_lp, float *out_logz) {
+    __shared__ float cv[256 * TOPK_MAX];
+    __shared__ int ci[256 * TOPK_MAX];
+    __shared__ float red[8];
+    __shared__ float selv[TOPK_MAX];
+    __shared__ int seli[TOPK_MAX];
+    __shared__ int wi[4], ws[4];
+    const int s = blockIdx.x;
+    if (active && !active[s]) return;
+    const float *x = cur + (size_t)s * V;
+    float tv[TOPK_MAX];
+    int ti[TOPK_MAX];
+    for (int j = 0; j < TOPK_MAX; j++) { tv[j] = -INFINITY; ti[j] = 0x7FFFFFFF; }
+    float mx = -INFINITY;
+    for (int i = threadIdx.x; i < V; i += blockDim.x) {
+        float v = x[i] * inv_temp;
+        mx = fmaxf(mx, v);
+        // insert into the local sorted list (value desc, index asc)
+        if (v > tv[k - 1] || (v == tv[k - 1] && i < ti[k - 1])) {
+            int j = k - 1;
+            while (j > 0 && (v > tv[j - 1] || (v == tv[j - 1] && i < ti[j - 1]))) {
+                tv[j] = tv[j - 1]; ti[j] = ti[j - 1]; j--;
+            }
+            tv[j] = v; ti[j] = i;
+        }
+    }
+    for (int j = 0; j < k; j++) { cv[threadIdx.x * TOPK_MAX + j] = tv[j]; ci[threadIdx.x * TOPK_MAX + j] = ti[j]; }
+    // global max
+    mx = group_max<64>(mx);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float es = 0.0f;
+    for (int i = threadIdx.x; i < V; i += blockDim.x) es += (float)exp((double)(x[i] * inv_temp - mx));
+    float sum = block_sum256(es, red);
+    const float logz = (float)log((double)sum) + mx;
+    // k rounds of block-wide selection over the 256*k candidates
+    for (int r = 0; r < k; r++) {
+        float bv = -INFINITY;
+        int bi = 0x7FFFFFFF, bslot = -1;
+        for (int j = 0; j < k; j++) {
+            int slot = threadIdx.x * TOPK_MAX + j;
+            float v = cv[slot];
+            int i = ci[slot];
+            if (i != 0x7FFFFFFF && (v > bv || (v == bv && i < bi))) { bv = v; bi = i; bslot = slot; }
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+            float ov = __shfl_xor(bv, o, 64);
+            int oi = __shfl_xor(bi, o, 64);
+            int os = __shfl_xor(bslot, o, 64);
+            if (oi != 0x7FFFFFFF && (ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; bslot = os; }
+        }
+        __syncthreads();
+        if (lane == 0) { red[wave] = bv; wi[wave] = bi; ws[wave] = bslot; }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float b0 = red[0];
+            int i0 = wi[0], s0 = ws[0];
+            for (int w = 1; w < 4; w++)
+                if (wi[w] != 0x7FFFFFFF && (red[w] > b0 || (red[w] == b0 && wi[w] < i0))) { b0 = red[w]; i0 = wi[w]; s0 = ws[w]; }
+            selv[r] = b0;
+            seli[r] = i0;
+            if (s0 >= 0) ci[s0] = 0x7FFFFFFF;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x < k) {
+        out_tok[(size_t)s * k + threadIdx.x] = seli[threadIdx.x];
+        out_lp[(size_t)s * k + threadIdx.x] = selv[threadIdx.x] - logz;
+    }
+    if (threadIdx.x == 0) out_logz[s] = logz;
+}
+
+int launch_topk(const float *cur, const int32_t *active, int S, int V, int k, float inv_temp, int32_t *out_tok,
+                float *out_lp, float *out_logz, hipStream_t st) {
+    if (k < 1 || k > TOPK_MAX) return fail(WH_ERR_INVALID, "topk: k must be in [1,8]");
+    hipLaunchKernelGGL(k_topk, dim3(S), dim3(256), 0, st, cur, active, V, k, inv_temp, out_tok, out_lp, out_logz);
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+}  // namespace wh

@@ -1,0 +1,673 @@
+// Decoder state in HBM and the token loop on the host
+// (internal/model/decoder.go:306-386 state, :413-525 greedy, :528-742 beam,
+// :745-993 forward). Only token ids (and, in parity mode, logits) cross PCIe.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "wh_internal.h"
+
+namespace wh {
+
+__global__ void k_zero_rows(float *base, size_t stride, int count, int len) {
+    for (int r = blockIdx.x; r < count; r += gridDim.x)
+        for (int j = threadIdx.x; j < len; j += blockDim.x) base[(size_t)r * stride + j] = 0.0f;
+}
+
+}  // namespace wh
+
+struct wh_seq {
+    const wh_model *m = nullptr;
+    int S = 0, enc_len = 0, n_enc = 0, hist_cap = 0;
+    hipStream_t st = nullptr;
+    std::vector<void *> allocs;
+    float *x = nullptr, *xln = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *h = nullptr;
+    float *logits = nullptr;
+    float *kv = nullptr;
+    size_t kv_stream = 0, kv_layer = 0;  // floats
+    float *crossK = nullptr, *crossV = nullptr;
+    const float **kbase = nullptr, **vbase = nullptr;  // [L][S] device pointer tables
+    wh::CrossBufs cb{};
+    wh::SampleBufs sb{};
+    int32_t *hist = nullptr, *hist_len = nullptr, *tok = nullptr, *pos = nullptr, *active = nullptr;
+    int32_t *out_ids = nullptr, *topk_tok = nullptr;
+    float *topk_lp = nullptr, *topk_logz = nullptr;
+    std::vector<int32_t> h_len;     // host mirror of hist_len
+    std::vector<int32_t> h_active;  // host mirror of active
+    int32_t *pinned_ids = nullptr;
+
+    // optional per-kernel timing: an event pair around every launch
+    struct ProfCat {
+        std::string name;
+        double ms = 0, bytes = 0;
+        int64_t launches = 0;
+    };
+    struct Pending {
+        hipEvent_t a, b;
+        int cat;
+        double bytes;
+    };
+    bool prof = false;
+    std::vector<ProfCat> prof_cats;
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> ev_pool;
+    size_t ev_next = 0;
+    hipEvent_t ev_get() {
+        if (ev_next == ev_pool.size()) {
+            hipEvent_t e;
+            if (hipEventCreate(&e) != hipSuccess) return nullptr;
+            ev_pool.push_back(e);
+        }
+        return ev_pool[ev_next++];
+    }
+    int cat_of(const char *name) {
+        for (size_t i = 0; i < prof_cats.size(); i++)
+            if (prof_cats[i].name == name) return (int)i;
+        prof_cats.push_back(ProfCat{name});
+        return (int)prof_cats.size() - 1;
+    }
+    void prof_resolve() {
+        for (auto &p : pending) {
+            float ms = 0;
+            if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+                prof_cats[p.cat].ms += ms;
+                prof_cats[p.cat].launches++;
+                prof_cats[p.cat].bytes += p.bytes;
+            }
+        }
+        pending.clear();
+        ev_next = 0;
+    }
+
+    ~wh_seq() {
+        if (st) (void)hipStreamSynchronize(st);
+        for (hipEvent_t e : ev_pool) (void)hipEventDestroy(e);
+        for (void *p : allocs) (void)hipFree(p);
+        if (pinned_ids) (void)hipHostFree(pinned_ids);
+        if (st) (void)hipStreamDestroy(st);
+    }
+    template <typename T>
+    int alloc(T **p, size_t count) {
+        void *d = nullptr;
+        size_t bytes = std::max<size_t>(count * sizeof(T), 256);
+        hipError_t e = hipMalloc(&d, bytes);
+        if (e != hipSuccess) return wh::fail(WH_ERR_NOMEM, std::string("hip: alloc: ") + hipGetErrorString(e));
+        allocs.push_back(d);
+        *p = (T *)d;
+        return WH_OK;
+    }
+};
+
+namespace wh {
+
+namespace {
+
+constexpr int SAMPLE_PARTS = 64;
+
+// Records an event pair around the launches in its scope when profiling is on;
+// `bytes` is the algorithmic HBM traffic of the launch.
+struct Prof {
+    wh_seq &s;
+    int cat = -1;
+    double bytes;
+    hipEvent_t a = nullptr;
+    Prof(wh_seq &s_, const char *name, double b) : s(s_), bytes(b) {
+        if (!s.prof) return;
+        cat = s.cat_of(name);
+        a = s.ev_get();
+        if (a) (void)hipEventRecord(a, s.st);
+    }
+    ~Prof() {
+        if (!s.prof || !a) return;
+        hipEvent_t b = s.ev_get();
+        if (!b) return;
+        (void)hipEventRecord(b, s.st);
+        s.pending.push_back({a, b, cat, bytes});
+    }
+};
+
+double mat_bytes(const DevMat &m) { return (double)m.algo_bytes; }
+
+int seq_forward(wh_seq &s) {
+    const wh_model &m = *s.m;
+    const int S = s.S, d = m.n_state, H = m.n_head, hd = d / H, ctx = m.n_ctx;
+    hipStream_t st = s.st;
+    int active = 0;
+    for (int i = 0; i < S; i++) active += s.h_active[i] != 0;
+    const double cross_kv_bytes = (double)active * s.enc_len * d * 4;  // one of K or V, per layer
+    int rc;
+    auto gemv1 = [&](const DevMat &w, const float *x, int ldx, float *y, int ldy, const float *bias, const float *res,
+                     int gelu) {
+        const DevMat *mat = &w;
+        GemvIn in{x, ldx};
+        GemvOut out;
+        out.y = y; out.ldy = ldy; out.bias = bias; out.res = res; out.ldres = ldy; out.gelu = gelu;
+        Prof p(s, "gemv", mat_bytes(w));
+        return launch_gemv(&mat, &in, &out, 1, S, st);
+    };
+    {
+        Prof p(s, "embed", 0);
+        if ((rc = launch_embed(m, s.tok, s.pos, s.active, s.x, S, st))) return rc;
+    }
+    for (int li = 0; li < m.n_layer; li++) {
+        const Layer &l = m.layers[li];
+        // self-attention sub-layer (decoder.go:780-790, :836-908)
+        {
+            Prof p(s, "layernorm", 0);
+            if ((rc = launch_layernorm(s.x, l.ln1w, l.ln1b, s.xln, S, d, st))) return rc;
+        }
+        if (l.sq.type == l.sk.type && l.sk.type == l.sv.type) {
+            const DevMat *mats[3] = {&l.sq, &l.sk, &l.sv};
+            GemvIn in[3] = {{s.xln, d}, {s.xln, d}, {s.xln, d}};
+            GemvOut out[3];
+            out[0].y = s.q; out[0].ldy = d; out[0].bias = l.sqb;
+            out[1].y = s.k; out[1].ldy = d;
+            out[2].y = s.v; out[2].ldy = d; out[2].bias = l.svb;
+            Prof p(s, "gemv", mat_bytes(l.sq) + mat_bytes(l.sk) + mat_bytes(l.sv));
+            if ((rc = launch_gemv(mats, in, out, 3, S, st))) return rc;
+        } else {
+            if ((rc = gemv1(l.sq, s.xln, d, s.q, d, l.sqb, nullptr, 0))) return rc;
+            if ((rc = gemv1(l.sk, s.xln, d, s.k, d, nullptr, nullptr, 0))) return rc;
+            if ((rc = gemv1(l.sv, s.xln, d, s.v, d, l.svb, nullptr, 0))) return rc;
+        }
+        {
+            Prof p(s, "self_attn", 0);
+            if ((rc = launch_self_attn(s.q, s.k, s.v, s.kv + (size_t)li * s.kv_layer, s.kv_stream, s.pos, s.active,
+                                       s.attn, S, H, hd, ctx, m.attn_mode, st)))
+                return rc;
+        }
+        if ((rc = gemv1(l.so, s.attn, d, s.x, d, l.sob, s.x, 0))) return rc;
+        // cross-attention sub-layer (decoder.go:792-801, :911-971)
+        {
+            Prof p(s, "layernorm", 0);
+            if ((rc = launch_layernorm(s.x, l.ln2w, l.ln2b, s.xln, S, d, st))) return rc;
+        }
+        if ((rc = gemv1(l.cq, s.xln, d, s.q, d, l.cqb, nullptr, 0))) return rc;
+        {
+            Prof p(s, "cross_attn", 2 * cross_kv_bytes);
+            if ((rc = launch_cross_attn(s.q, s.kbase + (size_t)li * S, s.vbase + (size_t)li * S, s.active, s.attn, S, H,
+                                        hd, s.enc_len, s.cb, st)))
+                return rc;
+        }
+        if ((rc = gemv1(l.co, s.attn, d, s.x, d, l.cob, s.x, 0))) return rc;
+        // MLP sub-layer (decoder.go:803-810, :974-993)
+        {
+            Prof p(s, "layernorm", 0);
+            if ((rc = launch_layernorm(s.x, l.ln3w, l.ln3b, s.xln, S, d, st))) return rc;
+        }
+        if ((rc = gemv1(l.fc1, s.xln, d, s.h, 4 * d, l.fc1b, nullptr, 1))) return rc;
+        if ((rc = gemv1(l.fc2, s.h, 4 * d, s.x, d, l.fc2b, s.x, 0))) return rc;
+    }
+    // final LN + tied logits (decoder.go:817-832)
+    {
+        Prof p(s, "layernorm", 0);
+        if ((rc = launch_layernorm(s.x, m.lnw, m.lnb, s.xln, S, d, st))) return rc;
+    }
+    return gemv1(m.tok, s.xln, d, s.logits, m.n_vocab, nullptr, nullptr, 0);
+}
+
+int check_positions(const wh_seq &s) {
+    for (int i = 0; i < s.S; i++) {
+        if (!s.h_active[i]) continue;
+        if (s.h_len[i] <= 0) return fail(WH_ERR_INVALID, "model: decode: forward: no tokens in state");
+        if (s.h_len[i] - 1 >= s.m->n_ctx)
+            return fail(WH_ERR_INVALID, "model: decode: forward: position " + std::to_string(s.h_len[i] - 1) +
+                                            " >= context length " + std::to_string(s.m->n_ctx));
+        if (s.h_len[i] + 1 > s.hist_cap) return fail(WH_ERR_INVALID, "model: decode: history capacity exceeded");
+    }
+    return WH_OK;
+}
+
+int upload_active(wh_seq &s, const int32_t *active) {
+    for (int i = 0; i < s.S; i++) s.h_active[i] = active ? (active[i] != 0) : 1;
+    WH_HIP(hipMemcpyAsync(s.active, s.h_active.data(), sizeof(int32_t) * s.S, hipMemcpyHostToDevice, s.st));
+    return WH_OK;
+}
+
+}  // namespace
+
+int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t enc_len, int32_t enc_dim,
+               int32_t shared, wh_seq **out) {
+    if (!m || !out) return fail(WH_ERR_INVALID, "seq: null argument");
+    *out = nullptr;
+    if (S < 1 || S > 16) return fail(WH_ERR_INVALID, "seq: n_streams must be in [1,16]");
+    if (enc_dim != m->n_state || enc_len <= 0)
+        return fail(WH_ERR_INVALID, "model: decoder: encoder output must be [T, " + std::to_string(m->n_state) +
+                                        "], got [" + std::to_string(enc_len) + " " + std::to_string(enc_dim) + "]");
+    if (!encs) return fail(WH_ERR_INVALID, "seq: null encoder outputs");
+    WH_HIP(hipSetDevice(m->device));
+    std::unique_ptr<wh_seq> s(new wh_seq());
+    s->m = m;
+    s->S = S;
+    s->enc_len = enc_len;
+    s->n_enc = shared ? 1 : S;
+    s->hist_cap = m->n_ctx + 64;
+    WH_HIP(hipStreamCreateWithFlags(&s->st, hipStreamNonBlocking));
+    const int d = m->n_state, H = m->n_head, hd = d / H, L = m->n_layer, V = m->n_vocab;
+    int rc;
+#define ALLOC(p, n) do { if ((rc = s->alloc(&(p), (n)))) return rc; } while (0)
+    ALLOC(s->x, (size_t)S * d);
+    ALLOC(s->xln, (size_t)S * d);
+    ALLOC(s->q, (size_t)S * d);
+    ALLOC(s->k, (size_t)S * d);
+    ALLOC(s->v, (size_t)S * d);
+    ALLOC(s->attn, (size_t)S * d);
+    ALLOC(s->h, (size_t)S * 4 * d);
+    ALLOC(s->logits, (size_t)S * V);
+    s->kv_layer = (size_t)2 * H * m->n_ctx * hd;
+    s->kv_stream = s->kv_layer * L;
+    ALLOC(s->kv, s->kv_stream * S);
+    WH_HIP(hipMemsetAsync(s->kv, 0, s->kv_stream * S * sizeof(float), s->st));
+    const size_t cross_per = (size_t)L * enc_len * d;
+    ALLOC(s->crossK, cross_per * s->n_enc);
+    ALLOC(s->crossV, cross_per * s->n_enc);
+    ALLOC(s->kbase, (size_t)L * S);
+    ALLOC(s->vbase, (size_t)L * S);
+    {
+        std::vector<const float *> kb((size_t)L * S), vb((size_t)L * S);
+        for (int li = 0; li < L; li++)
+            for (int i = 0; i < S; i++) {
+                const int e = shared ? 0 : i;
+                kb[(size_t)li * S + i] = s->crossK + ((size_t)e * L + li) * enc_len * d;
+                vb[(size_t)li * S + i] = s->crossV + ((size_t)e * L + li) * enc_len * d;
+            }
+        WH_HIP(hipMemcpy(s->kbase, kb.data(), kb.size() * sizeof(void *), hipMemcpyHostToDevice));
+        WH_HIP(hipMemcpy(s->vbase, vb.data(), vb.size() * sizeof(void *), hipMemcpyHostToDevice));
+    }
+    s->cb.chunk_len = 128;
+    s->cb.chunks = (enc_len + 127) / 128;
+    ALLOC(s->cb.scores, (size_t)S * H * enc_len);
+    ALLOC(s->cb.cmax, (size_t)S * H * s->cb.chunks);
+    ALLOC(s->cb.psum, (size_t)S * H * s->cb.chunks);
+    ALLOC(s->cb.pv, (size_t)S * H * s->cb.chunks * 64);
+    s->sb.parts = SAMPLE_PARTS;
+    ALLOC(s->sb.cur, (size_t)S * V);
+    ALLOC(s->sb.part_val, (size_t)S * SAMPLE_PARTS);
+    ALLOC(s->sb.part_idx, (size_t)S * SAMPLE_PARTS);
+    ALLOC(s->sb.part_val2, (size_t)S * SAMPLE_PARTS);
+    ALLOC(s->sb.part_idx2, (size_t)S * SAMPLE_PARTS);
+    ALLOC(s->hist, (size_t)S * s->hist_cap);
+    ALLOC(s->hist_len, (size_t)S);
+    ALLOC(s->tok, (size_t)S);
+    ALLOC(s->pos, (size_t)S);
+    ALLOC(s->active, (size_t)S);
+    ALLOC(s->out_ids, (size_t)S);
+    ALLOC(s->topk_tok, (size_t)S * 8);
+    ALLOC(s->topk_lp, (size_t)S * 8);
+    ALLOC(s->topk_logz, (size_t)S);
+#undef ALLOC
+    WH_HIP(hipMemsetAsync(s->hist_len, 0, sizeof(int32_t) * S, s->st));
+    WH_HIP(hipMemsetAsync(s->tok, 0, sizeof(int32_t) * S, s->st));
+    WH_HIP(hipMemsetAsync(s->pos, 0, sizeof(int32_t) * S, s->st));
+    // pinned staging: ids/top-k tokens [16*8], top-k logprobs [16*8], log-normalisers [16]
+    WH_HIP(hipHostMalloc((void **)&s->pinned_ids, sizeof(int32_t) * (16 * 8 * 2 + 16), hipHostMallocDefault));
+    s->h_len.assign(S, 0);
+    s->h_active.assign(S, 1);
+    // cross K/V projections of every encoder output (decoder.go:923-940), once per sequence
+    float *enc = nullptr;
+    WH_HIP(hipMalloc(&enc, sizeof(float) * (size_t)enc_len * d));
+    for (int e = 0; e < s->n_enc; e++) {
+        if (!encs[e]) { (void)hipFree(enc); return fail(WH_ERR_INVALID, "seq: null encoder output"); }
+        hipError_t he = hipMemcpyAsync(enc, encs[e], sizeof(float) * (size_t)enc_len * d, hipMemcpyHostToDevice, s->st);
+        if (he != hipSuccess) { (void)hipFree(enc); return fail(WH_ERR_HIP, "hip: encoder upload failed"); }
+        for (int li = 0; li < L; li++) {
+            const Layer &l = m->layers[li];
+            float *K = s->crossK + ((size_t)e * L + li) * enc_len * d;
+            float *Vv = s->crossV + ((size_t)e * L + li) * enc_len * d;
+            if ((rc = launch_cross_gemm(l.ck, enc, enc_len, nullptr, K, s->st)) ||
+                (rc = launch_cross_gemm(l.cv, enc, enc_len, l.cvb, Vv, s->st))) {
+                (void)hipStreamSynchronize(s->st);
+                (void)hipFree(enc);
+                return rc;
+            }
+        }
+        (void)hipStreamSynchronize(s->st);  // enc is reused for the next stream
+    }
+    (void)hipFree(enc);
+    WH_HIP(hipStreamSynchronize(s->st));
+    *out = s.release();
+    return WH_OK;
+}
+
+int seq_set_tokens(wh_seq *s, int32_t i, const int32_t *tokens, int32_t n, int32_t reset_kv) {
+    if (!s || i < 0 || i >= s->S) return fail(WH_ERR_INVALID, "seq: stream index out of range");
+    if (n < 0 || n > s->hist_cap - 1 || (n > 0 && !tokens)) return fail(WH_ERR_INVALID, "seq: invalid token history");
+    for (int j = 0; j < n; j++)
+        if (tokens[j] < 0 || tokens[j] >= s->m->n_vocab)
+            return fail(WH_ERR_INVALID, "model: decode: forward: invalid token ID " + std::to_string(tokens[j]));
+    WH_HIP(hipSetDevice(s->m->device));
+    if (n > 0)
+        WH_HIP(hipMemcpyAsync(s->hist + (size_t)i * s->hist_cap, tokens, sizeof(int32_t) * n, hipMemcpyHostToDevice, s->st));
+    int32_t meta[3] = {n, n > 0 ? tokens[n - 1] : 0, n > 0 ? n - 1 : 0};
+    // the three scalars are copied from a host array that outlives the call (synchronised below)
+    WH_HIP(hipMemcpyAsync(s->hist_len + i, &meta[0], 4, hipMemcpyHostToDevice, s->st));
+    WH_HIP(hipMemcpyAsync(s->tok + i, &meta[1], 4, hipMemcpyHostToDevice, s->st));
+    WH_HIP(hipMemcpyAsync(s->pos + i, &meta[2], 4, hipMemcpyHostToDevice, s->st));
+    if (reset_kv) {
+        const wh_model &m = *s->m;
+        float *base = s->kv + (size_t)i * s->kv_stream;
+        if (m.attn_mode == 0) {
+            // only cache row 0 is ever read under the reference mask: clear it in
+            // every (layer, K/V plane, head)
+            const int hd = m.n_state / m.n_head;
+            const int count = m.n_layer * 2 * m.n_head;
+            hipLaunchKernelGGL(k_zero_rows, dim3(std::min(count, 1024)), dim3(64), 0, s->st, base,
+                               (size_t)m.n_ctx * hd, count, hd);
+            WH_HIP(hipGetLastError());
+        } else {
+            WH_HIP(hipMemsetAsync(base, 0, s->kv_stream * sizeof(float), s->st));
+        }
+    }
+    WH_HIP(hipStreamSynchronize(s->st));
+    s->h_len[i] = n;
+    return WH_OK;
+}
+
+static int seq_forward_active(wh_seq *s, const int32_t *active) {
+    int rc;
+    if ((rc = upload_active(*s, active))) return rc;
+    if ((rc = check_positions(*s))) return rc;
+    return seq_forward(*s);
+}
+
+int seq_step_greedy(wh_seq *s, const int32_t *active, float temperature, int32_t suppress_nst, float nst,
+                    int32_t *out_ids, float *out_logits) {
+    if (!s) return fail(WH_ERR_INVALID, "seq: null handle");
+    WH_HIP(hipSetDevice(s->m->device));
+    int rc;
+    if ((rc = seq_forward_active(s, active))) return rc;
+    const float inv = temperature > 0 ? 1.0f / temperature : 1.0f;
+    const int V = s->m->n_vocab;
+    {
+        Prof p(*s, "sample", 0);
+        if ((rc = launch_penalty_argmax(s->logits, s->hist, s->hist_len, s->hist_cap, s->active, s->S, V, inv,
+                                        s->m->eot, s->sb, s->st)))
+            return rc;
+        if ((rc = launch_argmax_final(s->sb, s->sb.cur, s->S, V, s->m->eot, suppress_nst, nst, s->active, s->hist,
+                                      s->hist_len, s->hist_cap, s->tok, s->pos, s->out_ids, s->st)))
+            return rc;
+    }
+    WH_HIP(hipMemcpyAsync(s->pinned_ids, s->out_ids, sizeof(int32_t) * s->S, hipMemcpyDeviceToHost, s->st));
+    if (out_logits)
+        WH_HIP(hipMemcpyAsync(out_logits, s->logits, sizeof(float) * (size_t)s->S * V, hipMemcpyDeviceToHost, s->st));
+    WH_HIP(hipStreamSynchronize(s->st));
+    if (s->prof) s->prof_resolve();
+    for (int i = 0; i < s->S; i++) {
+        if (out_ids) out_ids[i] = s->h_active[i] ? s->pinned_ids[i] : -1;
+        if (s->h_active[i]) s->h_len[i]++;
+    }
+    return WH_OK;
+}
+
+int seq_step_topk(wh_seq *s, const int32_t *active, int32_t k, float temperature, int32_t *out_tok, float *out_lp,
+                  float *out_logits) {
+    if (!s) return fail(WH_ERR_INVALID, "seq: null handle");
+    if (k < 1 || k > 8) return fail(WH_ERR_INVALID, "seq: k must be in [1,8]");
+    WH_HIP(hipSetDevice(s->m->device));
+    int rc;
+    if ((rc = seq_forward_active(s, active))) return rc;
+    const float inv = temperature > 0 ? 1.0f / temperature : 1.0f;
+    const int V = s->m->n_vocab;
+    // the penalised copy `cur` is produced by the same pass that feeds greedy
+    // selection; its argmax partials are unused here
+    if ((rc = launch_penalty_argmax(s->logits, s->hist, s->hist_len, s->hist_cap, s->active, s->S, V, inv, s->m->eot,
+                                    s->sb, s->st)))
+        return rc;
+    // one extra candidate exposes a tie at the k-th place
+    const int kk = std::min(k + 1, 8);
+    if ((rc = launch_topk(s->sb.cur, s->active, s->S, V, kk, inv, s->topk_tok, s->topk_lp, s->topk_logz, s->st)))
+        return rc;
+    int32_t *h_tok = s->pinned_ids;
+    float *h_lp = (float *)(s->pinned_ids + 16 * 8);
+    float *h_logz = (float *)(s->pinned_ids + 2 * 16 * 8);
+    WH_HIP(hipMemcpyAsync(h_tok, s->topk_tok, sizeof(int32_t) * s->S * kk, hipMemcpyDeviceToHost, s->st));
+    WH_HIP(hipMemcpyAsync(h_lp, s->topk_lp, sizeof(float) * s->S * kk, hipMemcpyDeviceToHost, s->st));
+    WH_HIP(hipMemcpyAsync(h_logz, s->topk_logz, sizeof(float) * s->S, hipMemcpyDeviceToHost, s->st));
+    if (out_logits)
+        WH_HIP(hipMemcpyAsync(out_logits, s->logits, sizeof(float) * (size_t)s->S * V, hipMemcpyDeviceToHost, s->st));
+    WH_HIP(hipStreamSynchronize(s->st));
+    if (s->prof) s->prof_resolve();
+    std::vector<float> row;
+    for (int i = 0; i < s->S; i++) {
+        const int32_t *t = h_tok + (size_t)i * kk;
+        const float *l = h_lp + (size_t)i * kk;
+        bool tie = false;
+        for (int j = 0; j + 1 < kk; j++) tie |= (l[j] == l[j + 1]);
+        if (s->h_active[i] && tie) {
+            // Equal values at or inside the k-th place: the kept set and its
+            // order depend on the reference's streaming replace-min scan
+            // (decoder.go:1089-1121) followed by a stable sort of <= 12 items
+            // (sort.Slice falls back to insertion sort there), so rerun that
+            // scan exactly over the penalised row.
+            row.resize(V);
+            WH_HIP(hipMemcpy(row.data(), s->sb.cur + (size_t)i * V, sizeof(float) * V, hipMemcpyDeviceToHost));
+            std::vector<int32_t> bt;
+            std::vector<float> bv;
+            int minpos = -1;
+            float minval = 0.0f;
+            for (int x = 0; x < V; x++) {
+                const float sc = row[x] * inv;
+                if ((int)bt.size() < k) {
+                    bt.push_back(x);
+                    bv.push_back(sc);
+                    if (minpos < 0 || sc < minval) { minpos = (int)bt.size() - 1; minval = sc; }
+                    continue;
+                }
+                if (sc <= minval) continue;
+                bt[minpos] = x;
+                bv[minpos] = sc;
+                minpos = 0;
+                minval = bv[0];
+                for (int j = 1; j < (int)bv.size(); j++)
+                    if (bv[j] < minval) { minval = bv[j]; minpos = j; }
+            }
+            std::vector<int> order(bt.size());
+            for (size_t j = 0; j < order.size(); j++) order[j] = (int)j;
+            for (size_t j = 0; j < bv.size(); j++) bv[j] -= h_logz[i];
+            std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return bv[a] > bv[b]; });
+            for (int j = 0; j < k; j++) {
+                out_tok[(size_t)i * k + j] = j < (int)order.size() ? bt[order[j]] : -1;
+                out_lp[(size_t)i * k + j] = j < (int)order.size() ? bv[order[j]] : 0.0f;
+            }
+            continue;
+        }
+        for (int j = 0; j < k; j++) {
+            out_tok[(size_t)i * k + j] = s->h_active[i] ? t[j] : -1;
+            out_lp[(size_t)i * k + j] = s->h_active[i] ? l[j] : 0.0f;
+        }
+    }
+    return WH_OK;
+}
+
+void seq_destroy(wh_seq *s) { delete s; }
+
+int seq_set_profiling(wh_seq *s, int32_t enable) {
+    if (!s) return fail(WH_ERR_INVALID, "seq: null handle");
+    WH_HIP(hipStreamSynchronize(s->st));
+    s->pending.clear();
+    s->ev_next = 0;
+    s->prof_cats.clear();
+    s->prof = enable != 0;
+    return WH_OK;
+}
+
+int seq_profile_get(wh_seq *s, int32_t i, char *name, int32_t cap, double *ms, int64_t *launches, double *bytes) {
+    if (!s) return fail(WH_ERR_INVALID, "seq: null handle");
+    if (i < 0 || i >= (int32_t)s->prof_cats.size()) return fail(WH_ERR_INVALID, "seq: profile index out of range");
+    const auto &c = s->prof_cats[i];
+    if (name && cap > 0) {
+        std::strncpy(name, c.name.c_str(), (size_t)cap - 1);
+        name[cap - 1] = 0;
+    }
+    if (ms) *ms = c.ms;
+    if (launches) *launches = c.launches;
+    if (bytes) *bytes = c.bytes;
+    return WH_OK;
+}
+
+int seq_profile_count(wh_seq *s, int32_t *n) {
+    if (!s || !n) return fail(WH_ERR_INVALID, "seq: null argument");
+    *n = (int32_t)s->prof_cats.size();
+    return WH_OK;
+}
+
+// ---- whole decode loops --------------------------------------------------------
+namespace {
+
+int cap_max_tokens(const wh_model &m, const wh_decode_params &p) {  // decoder.go:420-430
+    int mt = p.max_tokens;
+    if (mt <= 0) mt = m.n_ctx;
+    if (m.n_ctx - p.prompt_len < mt) mt = m.n_ctx - p.prompt_len;
+    return std::max(mt, 0);
+}
+
+int check_params(const wh_model &m, const wh_decode_params *p) {
+    if (!p) return fail(WH_ERR_INVALID, "model: decode: null params");
+    if (p->prompt_len < 0 || (p->prompt_len > 0 && !p->prompt)) return fail(WH_ERR_INVALID, "model: decode: invalid prompt");
+    const float base = p->temperature == 0 ? 1.0f : p->temperature;
+    if (p->logprob_thold > 0 && !p->no_fallback && base > 0)
+        return fail(WH_ERR_UNSUPPORTED,
+                    "model: decode: top-p fallback (LogprobThold > 0 without NoFallback) is non-deterministic in the "
+                    "reference and is not supported");
+    return WH_OK;
+}
+
+bool cancelled(const volatile int32_t *c) { return c && *c != 0; }
+
+}  // namespace
+
+// decoder.go:413-525 for n_streams independent streams (no vocabulary: no
+// compression-ratio retries).
+int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, int32_t enc_len, int32_t enc_dim,
+                        const wh_decode_params *params, int32_t *out_tokens, int32_t cap, int32_t *out_lens,
+                        const volatile int32_t *cancel) {
+    int rc;
+    for (int i = 0; i < S; i++)
+        if ((rc = check_params(*m, &params[i]))) return rc;
+    wh_seq *sp = nullptr;
+    if ((rc = seq_create(m, S, encs, enc_len, enc_dim, 0, &sp))) return rc;
+    std::unique_ptr<wh_seq, void (*)(wh_seq *)> s(sp, seq_destroy);
+    std::vector<std::vector<int32_t>> toks(S);
+    std::vector<int32_t> active(S, 1), maxt(S), streak(S, 0), prev(S, -1), ids(S);
+    for (int i = 0; i < S; i++) {
+        const wh_decode_params &p = params[i];
+        toks[i].assign(p.prompt, p.prompt + p.prompt_len);
+        maxt[i] = cap_max_tokens(*m, p);
+        if ((rc = seq_set_tokens(s.get(), i, p.prompt, p.prompt_len, 0))) return rc;
+        if ((int)toks[i].size() >= p.prompt_len + maxt[i]) active[i] = 0;
+        else if (p.prompt_len == 0) return fail(WH_ERR_INVALID, "model: decode: forward: no tokens in state");
+    }
+    // one temperature / suppress setting per call: streams share the first params
+    const wh_decode_params &p0 = params[0];
+    const float base = p0.temperature == 0 ? 1.0f : p0.temperature;
+    while (std::any_of(active.begin(), active.end(), [](int32_t a) { return a != 0; })) {
+        if (cancelled(cancel)) return fail(WH_ERR_CANCELLED, "model: decode: cancelled: context canceled");
+        if ((rc = seq_step_greedy(s.get(), active.data(), base, p0.suppress_nst, p0.no_speech_thold, ids.data(), nullptr)))
+            return fail(rc, std::string("model: decode: forward: ") + wh_last_error());
+        for (int i = 0; i < S; i++) {
+            if (!active[i]) continue;
+            const int32_t next = ids[i];
+            toks[i].push_back(next);
+            if (next == m->eot) { active[i] = 0; continue; }
+            if (prev[i] == next) streak[i]++;
+            else { streak[i] = 1; prev[i] = next; }
+            if (streak[i] > 20) { active[i] = 0; continue; }
+            if ((int)toks[i].size() >= params[i].prompt_len + maxt[i]) active[i] = 0;
+        }
+    }
+    for (int i = 0; i < S; i++) {
+        if ((int)toks[i].size() > cap) return fail(WH_ERR_INVALID, "model: decode: output capacity too small");
+        std::memcpy(out_tokens + (size_t)i * cap, toks[i].data(), toks[i].size() * sizeof(int32_t));
+        out_lens[i] = (int32_t)toks[i].size();
+    }
+    return WH_OK;
+}
+
+// decoder.go:528-726. The beam_size hypotheses run as one batch; every
+// hypothesis is reset before its forward (P9), the cross K/V are shared and
+// computed once (the reference recomputes identical values each step).
+// Candidates are ordered by normalised score with a stable tie-break
+// (insertion order) where Go's sort.Slice is unstable.
+int decode_beam(const wh_model *m, const float *enc, int32_t enc_len, int32_t enc_dim, const wh_decode_params *p,
+                int32_t *out_tokens, int32_t cap, int32_t *out_len, const volatile int32_t *cancel) {
+    int rc;
+    if ((rc = check_params(*m, p))) return rc;
+    const float temp = p->temperature == 0 ? 1.0f : p->temperature;
+    const int bs = std::min(p->beam_size <= 0 ? 1 : p->beam_size, 16);
+    const int mt = cap_max_tokens(*m, *p);
+    std::vector<const float *> encs(bs, enc);
+    wh_seq *sp = nullptr;
+    if ((rc = seq_create(m, bs, encs.data(), enc_len, enc_dim, 1, &sp))) return rc;
+    std::unique_ptr<wh_seq, void (*)(wh_seq *)> s(sp, seq_destroy);
+    struct Beam { std::vector<int32_t> tokens; float score; };
+    struct Cand { int parent; float score; int32_t token; float logprob; float norm; };
+    std::vector<Beam> beams(bs, Beam{std::vector<int32_t>(p->prompt, p->prompt + p->prompt_len), 0.0f});
+    std::vector<int32_t> active(bs), ttok((size_t)bs * 5);
+    std::vector<float> tlp((size_t)bs * 5);
+    for (int step = 0; step < mt; step++) {
+        if (cancelled(cancel)) return fail(WH_ERR_CANCELLED, "model: decode: beam search cancelled: context canceled");
+        std::vector<Cand> cands;
+        bool any = false;
+        for (int b = 0; b < (int)beams.size(); b++) {
+            const Beam &h = beams[b];
+            active[b] = !(h.tokens.size() > 0 && h.tokens.back() == m->eot);
+            if (active[b]) {
+                if (h.tokens.empty()) return fail(WH_ERR_INVALID, "model: decode: beam search forward: no tokens in state");
+                if ((rc = seq_set_tokens(s.get(), b, h.tokens.data(), (int32_t)h.tokens.size(), 1))) return rc;
+                any = true;
+            }
+        }
+        for (int b = (int)beams.size(); b < bs; b++) active[b] = 0;
+        if (any && (rc = seq_step_topk(s.get(), active.data(), 5, temp, ttok.data(), tlp.data(), nullptr)))
+            return fail(rc, std::string("model: decode: beam search forward: ") + wh_last_error());
+        for (int b = 0; b < (int)beams.size(); b++) {
+            const Beam &h = beams[b];
+            if (!active[b]) {
+                const float norm = h.score / (float)std::pow((double)h.tokens.size(), 0.6);
+                cands.push_back({b, h.score, m->eot, 0.0f, norm});
+                continue;
+            }
+            const int nl = (int)h.tokens.size() + 1;
+            for (int c = 0; c < 5; c++) {
+                const float ns = h.score + tlp[(size_t)b * 5 + c];
+                cands.push_back({b, ns, ttok[(size_t)b * 5 + c], tlp[(size_t)b * 5 + c], ns / (float)std::pow((double)nl, 0.6)});
+            }
+        }
+        std::stable_sort(cands.begin(), cands.end(), [](const Cand &a, const Cand &b) { return a.norm > b.norm; });
+        const int keep = std::min<int>((int)cands.size(), bs);
+        std::vector<Beam> next(keep);
+        for (int i = 0; i < keep; i++) {
+            const Cand &c = cands[i];
+            const Beam &par = beams[c.parent];
+            next[i].tokens = par.tokens;
+            const bool carry = !par.tokens.empty() && par.tokens.back() == m->eot && c.token == m->eot && c.logprob == 0;
+            if (!carry) next[i].tokens.push_back(c.token);
+            next[i].score = c.score;
+        }
+        beams.swap(next);
+        bool all_eot = true;
+        for (auto &h : beams)
+            if (h.tokens.empty() || h.tokens.back() != m->eot) { all_eot = false; break; }
+        if (all_eot) break;
+        if (!beams.empty() && beams[0].tokens.size() >= 2) {
+            const auto &t = beams[0].tokens;
+            int streak = 1;
+            bool stop = false;
+            for (int i = (int)t.size() - 2; i >= 0 && t[i] == t.back(); i--)
+                if (++streak > 20) { stop = true; break; }
+            if (stop) break;
+        }
+    }
+    if (beams.empty()) { *out_len = 0; return WH_OK; }
+    if ((int)beams[0].tokens.size() > cap) return fail(WH_ERR_INVALID, "model: decode: output capacity too small");
+    std::memcpy(out_tokens, beams[0].tokens.data(), beams[0].tokens.size() * sizeof(int32_t));
+    *out_len = (int32_t)beams[0].tokens.size();
+    return WH_OK;
+}
+
+}  // namespace wh
