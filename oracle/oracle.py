@@ -130,10 +130,11 @@ def gemv(qtype, w, rows, cols, a, variant=1, threads=1):
 
 def layernorm(x, w, b, eps=1e-5):
     x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
     out = np.empty_like(x)
     c = x.shape[-1]
-    lib().or_layernorm(_p(out), _p(x), _p(np.ascontiguousarray(w, np.float32)),
-                       _p(np.ascontiguousarray(b, np.float32)), x.size // c, c, eps)
+    lib().or_layernorm(_p(out), _p(x), _p(w), _p(b), x.size // c, c, eps)
     return out
 
 

@@ -1,0 +1,171 @@
+"""The oracle decoder (forward + Decode loops) pinned against an independent
+float64 numpy restatement of internal/model/decoder.go:745-993 and against the
+behaviours of internal/model/decoder_test.go."""
+import math
+
+import numpy as np
+import pytest
+
+
+def _deq(orc, t):
+    n = int(np.prod(t.shape))
+    return orc.dequantize(t.data, t.type, n).astype(np.float64).reshape(t.shape)
+
+
+def _ln(x, w, b):
+    return (x - x.mean()) / np.sqrt(x.var() + 1e-5) * w + b
+
+
+def _gelu(x):
+    return 0.5 * x * (1 + np.tanh(math.sqrt(2 / math.pi) * (x + 0.044715 * x ** 3)))
+
+
+class NumpyDecoder:
+    """decoder.go restated in float64 with exact softmax. Self-attention
+    follows P1/P2: only KV-cache row 0 is attended (it holds k,v only when
+    the forward ran at position 0). Cross-attention follows P3: head h, key t
+    reads row h*(T/H) + t//H, columns (t%H)*hd ... +hd of the [T, d] projection."""
+
+    def __init__(self, orc, tensors, meta):
+        self.W = {t.name: _deq(orc, t) for t in tensors}
+        self.H, self.L, self.d = meta["n_head"], meta["n_layer"], meta["n_state"]
+        self.row0_v = None
+
+    def forward(self, tokens, enc):
+        W, H, d = self.W, self.H, self.d
+        hd = d // H
+        pos = len(tokens) - 1
+        x = W["decoder.token_embedding.weight"][tokens[-1]] + W["decoder.positional_embedding"][pos]
+        enc = enc.astype(np.float64)
+        T = enc.shape[0]
+        if pos == 0:
+            self.row0_v = [None] * self.L
+        for i in range(self.L):
+            p = f"decoder.blocks.{i}."
+            xl = _ln(x, W[p + "self_attn_ln.weight"], W[p + "self_attn_ln.bias"])
+            v = W[p + "self_attn.value.weight"] @ xl + W[p + "self_attn.value.bias"]
+            if pos == 0:
+                self.row0_v[i] = v
+            attn = self.row0_v[i] if self.row0_v is not None and self.row0_v[i] is not None else np.zeros(d)
+            x = x + (W[p + "self_attn.out.weight"] @ attn + W[p + "self_attn.out.bias"])
+            xl = _ln(x, W[p + "cross_attn_ln.weight"], W[p + "cross_attn_ln.bias"])
+            q = W[p + "cross_attn.query.weight"] @ xl + W[p + "cross_attn.query.bias"]
+            K = enc @ W[p + "cross_attn.key.weight"].T
+            V = enc @ W[p + "cross_attn.value.weight"].T + W[p + "cross_attn.value.bias"]
+            out = np.zeros(d)
+            for h in range(H):
+                rows = h * (T // H) + np.arange(T) // H
+                cols = (np.arange(T) % H)[:, None] * hd + np.arange(hd)[None, :]
+                Kh, Vh = K[rows[:, None], cols], V[rows[:, None], cols]
+                s = Kh @ q[h * hd:(h + 1) * hd] / math.sqrt(hd)
+                pr = np.exp(s - s.max())
+                pr /= pr.sum()
+                out[h * hd:(h + 1) * hd] = pr @ Vh
+            x = x + (W[p + "cross_attn.out.weight"] @ out + W[p + "cross_attn.out.bias"])
+            xl = _ln(x, W[p + "mlp_ln.weight"], W[p + "mlp_ln.bias"])
+            hmid = _gelu(W[p + "mlp.0.weight"] @ xl + W[p + "mlp.0.bias"])
+            x = x + (W[p + "mlp.2.weight"] @ hmid + W[p + "mlp.2.bias"])
+        x = _ln(x, W["decoder.ln.weight"], W["decoder.ln.bias"])
+        return W["decoder.token_embedding.weight"] @ x
+
+
+@pytest.mark.parametrize("qtype", [8, 3, 0])
+@pytest.mark.parametrize("prompt", [[11], [4, 5, 6]])
+def test_forward_matches_numpy_restatement(wh, orc, qtype, prompt):
+    dims = (300, 128, 4, 2, 16)
+    tensors, meta = wh.synth.make_decoder(f"np{qtype}", qtype, dims=dims)
+    enc = wh.synth.encoder_output(f"np{qtype}", 128, enc_len=40)
+    ref = orc.OracleModel(tensors, meta)
+    ref.set_fast_exp(False)
+    npd = NumpyDecoder(orc, tensors, meta)
+    st = ref.state(prompt)
+    toks = list(prompt)
+    for step in range(3):
+        got = st.forward(enc)
+        want = npd.forward(toks, enc)
+        assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 2e-5, (qtype, prompt, step)
+        nxt = int(np.argmax(got))
+        st.push(nxt)
+        toks.append(nxt)
+
+
+def test_fast_exp_is_used_by_default(wh, orc):
+    """The reference softmax default is the fast exp (attention.go:14): logits
+    differ from the exact-exp forward by more than rounding."""
+    tensors, meta = wh.synth.make_decoder("fx", 8, dims=(300, 128, 2, 1, 16))
+    enc = wh.synth.encoder_output("fx", 128, enc_len=40)
+    ref = orc.OracleModel(tensors, meta)
+    a = ref.state([3]).forward(enc)
+    ref.set_fast_exp(False)
+    b = ref.state([3]).forward(enc)
+    diff = np.max(np.abs(a - b)) / np.max(np.abs(b))
+    assert 1e-7 < diff < 1e-3
+
+
+def test_prompt_prefix_only_matters_through_penalty(wh, orc):
+    """P2: the prompt is never prefilled, so with the same last token and
+    length the first-step logits do not depend on earlier prompt tokens."""
+    tensors, meta = wh.synth.make_decoder("p2", 8, dims=(300, 128, 2, 2, 16))
+    enc = wh.synth.encoder_output("p2", 128, enc_len=40)
+    ref = orc.OracleModel(tensors, meta)
+    a = ref.state([1, 2, 3, 9]).forward(enc)
+    b = ref.state([7, 7, 250, 9]).forward(enc)
+    assert np.array_equal(a, b)
+
+
+def _fixture(wh, orc):
+    tensors, meta = wh.synth.reference_test_decoder()
+    return orc.OracleModel(tensors, meta), np.full((8, 4), 0.01, np.float32)
+
+
+def test_reference_fixture_greedy_and_beam(wh, orc):
+    """decoder_test.go:89-180: greedy and beam return a segment with tokens."""
+    ref, enc = _fixture(wh, orc)
+    for beam in (1, 3):
+        p = wh.DecoderParams(prompt=[50258, 50259, 50357, 50363], beam_size=beam, max_tokens=5, temperature=1.0)
+        toks = ref.decode(enc, p)
+        segs = wh.tokens_to_segments(toks, p.prompt)
+        assert len(segs) == 1 and 0 < len(segs[0].tokens) <= 5
+
+
+def test_max_tokens_capping(wh, orc):
+    """decoder.go:420-430: maxTokens defaults to n_text_ctx and is capped to
+    n_text_ctx - len(prompt)."""
+    tensors, meta = wh.synth.make_decoder("cap", 8, dims=(300, 64, 1, 1, 12))
+    enc = wh.synth.encoder_output("cap", 64, enc_len=10)
+    ref = orc.OracleModel(tensors, meta)
+    ref.set_eot(-1)  # never stop on EOT
+    for mt, plen, want in [(0, 3, 9), (5, 3, 5), (50, 10, 2), (4, 12, 0), (0, 13, 0)]:
+        p = wh.DecoderParams(prompt=list(range(1, plen + 1)), max_tokens=mt, no_fallback=True)
+        toks = ref.decode(enc, p)
+        gen = len(toks) - plen
+        # a streak of > 20 repeats may stop earlier; with these caps it cannot
+        assert gen == want, (mt, plen, gen)
+
+
+def test_eot_stops_greedy(wh, orc):
+    tensors, meta = wh.synth.make_decoder("eot", 8, dims=(300, 64, 1, 1, 40))
+    enc = wh.synth.encoder_output("eot", 64, enc_len=10)
+    ref = orc.OracleModel(tensors, meta)
+    p = wh.DecoderParams(prompt=[1], max_tokens=20, no_fallback=True)
+    free = ref.decode(enc, p)
+    stop_tok = free[3]
+    ref.set_eot(stop_tok)
+    toks = ref.decode(enc, p)
+    assert toks[-1] == stop_tok and toks == free[:len(toks)] and len(toks) <= 4
+
+
+def test_topp_fallback_is_rejected(wh, orc):
+    tensors, meta = wh.synth.make_decoder("tp", 8, dims=(300, 64, 1, 1, 12))
+    enc = wh.synth.encoder_output("tp", 64, enc_len=10)
+    ref = orc.OracleModel(tensors, meta)
+    with pytest.raises(RuntimeError, match="top-p"):
+        ref.decode(enc, wh.DecoderParams(prompt=[1], logprob_thold=1.0, max_tokens=2))
+
+
+def test_tokens_to_segments(wh):
+    """decoder.go:1415-1459 without a vocabulary."""
+    assert wh.tokens_to_segments([1, 2], [1, 2, 3]) == []
+    assert wh.tokens_to_segments([1, 2, 3], [1, 2, 3]) == []
+    segs = wh.tokens_to_segments([1, 2, 3, 9, 9], [1, 2, 3])
+    assert [t.id for t in segs[0].tokens] == [9, 9] and segs[0].text == ""

@@ -267,6 +267,10 @@ int wh_matrix_create(uint32_t type, int32_t rows, int32_t cols, const void *raw,
     wh_matrix *w = new wh_matrix();
     w->device = device;
     int rc = devmat_plan(w->m, type, rows, cols);
+    const uint64_t need = (uint64_t)rows * gguf_row_bytes(type, (uint64_t)cols);
+    if (!rc && nbytes < need)
+        rc = fail(WH_ERR_INVALID,
+                  "NewQuantizedMatrix: short data got=" + std::to_string(nbytes) + " need=" + std::to_string(need));
     if (!rc) {
         hipError_t e = hipSetDevice(device);
         rc = e == hipSuccess ? devmat_upload_typed(w->m, type, (const uint8_t *)raw, nbytes)
