@@ -64,6 +64,18 @@ def cpu_baseline(wh, tensors, meta, enc, prompt, n_tokens, gpu_tokens):
             "tokens_match_gpu": gen == gpu_tokens[:len(gen)]}
 
 
+def generate_n(seq, n):
+    """n greedy tokens of stream 0; generate() stops early on the reference's
+    stop rules (EOT, repeats), so call it again until n tokens exist."""
+    out = []
+    while len(out) < n:
+        got = seq.generate(n - len(out))
+        if not got:
+            raise SystemExit("bench: generate made no progress")
+        out += got
+    return out
+
+
 def run_decode(args):
     wh = __graft_entry__.load_package()
     if wh.native.device_count() < 1:
@@ -76,33 +88,33 @@ def run_decode(args):
     prompt = list(wh.synth.SOT_EN_TRANSCRIBE)
     wbytes = wh.synth.weight_bytes_per_token(tensors)
     log(f"bench: model {args.config} {args.qtype} generated in {time.time() - t0:.1f}s, {wbytes} weight B/token")
-    t0 = time.time()
-    dec = wh.HIPDecoder(tensors, meta, device=0)
-    seq = dec.sequence([enc])
-    seq.set_tokens(0, prompt)
-    log(f"bench: uploaded + cross K/V in {time.time() - t0:.2f}s")
-    total = args.warmup + args.steps + args.profile_steps
+    total = args.warmup + args.steps
     if len(prompt) + total > meta["n_ctx"]:
         raise SystemExit(f"bench: {total} steps exceed n_text_ctx {meta['n_ctx']}")
-    tokens = []
-    for _ in range(args.warmup):
-        tokens.append(seq.step_greedy()[0])
+    t0 = time.time()
+    dec = wh.HIPDecoder(tensors, meta, device=0)
+    if dec.weight_bytes != wbytes:
+        raise SystemExit(f"bench: device weight bytes {dec.weight_bytes} != {wbytes}")
+    seq = dec.sequence([enc])
+    seq.set_tokens(0, prompt)
+    persistent = seq.persistent[0]
+    log(f"bench: uploaded + cross K/V in {time.time() - t0:.2f}s, persistent kernel: {persistent}")
     t1 = time.perf_counter()
-    for _ in range(args.steps):
-        tokens.append(seq.step_greedy()[0])
-    dt = time.perf_counter() - t1
-    log(f"bench: {args.steps} steps in {dt * 1e3:.1f} ms")
-    # profiled pass: event pair around every launch
+    tokens = generate_n(seq, 1)
+    first_ms = (time.perf_counter() - t1) * 1e3
+    tokens += generate_n(seq, args.warmup - 1) if args.warmup > 1 else []
+    # timed region: HIP events around each launch give the kernel's own time
     seq.set_profiling(True)
-    for _ in range(args.profile_steps):
-        tokens.append(seq.step_greedy()[0])
+    launches0 = seq.persistent[1]
+    t1 = time.perf_counter()
+    timed = generate_n(seq, args.steps)
+    dt = time.perf_counter() - t1
     prof = seq.profile()
+    launches = seq.persistent[1] - launches0
     seq.set_profiling(False)
-    stop = None
-    for i, t in enumerate(tokens):
-        if t == dec.eot:
-            stop = i + 1
-            break
+    tokens += timed
+    seq.close()
+    log(f"bench: {args.steps} steps in {dt * 1e3:.1f} ms ({launches} persistent launches)")
     kern_ms = {k: v[0] for k, v in prof.items()}
     dom = max(kern_ms, key=kern_ms.get)
     dms, dcount, dbytes = prof[dom]
@@ -113,20 +125,34 @@ def run_decode(args):
         else f"decode tokens/s ({args.config} {args.qtype}, bs=1)",
         "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(dt * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "f32 activations, " + args.qtype + " weights", "data": "synthetic",
-        "config": {"workload": f"whisper {args.config} decoder, {args.qtype}, greedy, batch 1, "
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"whisper {args.config} decoder, {args.qtype} weights, greedy, batch 1, "
                                f"1500x{d} synthetic encoder output", "global_batch": 1,
-                   "prompt": prompt, "steps_timed": args.steps},
+                   "prompt": prompt, "steps_timed": args.steps, "weights": args.qtype},
+        "path": "persistent" if persistent else "multi-kernel",
+        "first_token_ms": round(first_ms, 3),
         "weight_bytes_per_token": wbytes,
         "weight_roofline_frac": round(wbytes * value / (HBM_PEAK_GBS * 1e9), 4),
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "launches": dcount, "avg_launch_us": round(dms * 1e3 / max(dcount, 1), 3),
                      "bytes_per_launch": round(dbytes / max(dcount, 1)), "traffic": None},
-        "kernel_ms_per_step": {k: round(v / args.profile_steps, 4) for k, v in kern_ms.items()},
-        "stopped_at_step": stop,
+        "kernel_ms_per_step": {k: round(v / args.steps, 4) for k, v in kern_ms.items()},
+        "stopped_at_step": next((i + 1 for i, t in enumerate(tokens) if t == dec.eot), None),
     }
-    seq.close()
+    if args.multikernel_steps > 0:
+        # the same tokens through one launch per kernel (the persistent kernel off)
+        os.environ["WHISPER_HIP_PERSISTENT"] = "0"
+        s0 = dec.sequence([enc])
+        del os.environ["WHISPER_HIP_PERSISTENT"]
+        s0.set_tokens(0, prompt)
+        mk = [s0.step_greedy()[0] for _ in range(4)]
+        t1 = time.perf_counter()
+        mk += [s0.step_greedy()[0] for _ in range(args.multikernel_steps)]
+        mdt = time.perf_counter() - t1
+        s0.close()
+        out["multikernel"] = {"tokens_per_s": round(args.multikernel_steps / mdt, 2),
+                              "tokens_match": mk == tokens[:len(mk)]}
     dec.close()
     if args.cpu_tokens > 0:
         log("bench: cpu baseline ...")
@@ -182,11 +208,12 @@ def run_gemv(args):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=216)
-    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--steps", type=int, default=224)
+    ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--config", default="large-v3")
     ap.add_argument("--qtype", default="Q8_0", choices=sorted(QNAMES))
-    ap.add_argument("--profile-steps", type=int, default=16)
+    ap.add_argument("--multikernel-steps", type=int, default=32,
+                    help="also time this many steps with one launch per kernel (0 = skip)")
     ap.add_argument("--cpu-tokens", type=int, default=3, help="oracle steps timed for cpu_baseline (0 = skip)")
     ap.add_argument("--gemv", action="store_true", help="run the standalone GEMV microbench instead")
     ap.add_argument("--gemv-formats", default="Q8_0,Q4_0,Q4_1,Q5_0,Q5_1")

@@ -204,6 +204,21 @@ int wh_seq_step_greedy(wh_seq *s, const int32_t *active, float temperature, int3
 int wh_seq_step_topk(wh_seq *s, const int32_t *active, int32_t k, float temperature, int32_t *out_tok,
                      float *out_logprob, float *out_logits);
 
+/* Up to n greedy steps of a one-stream sequence with the reference's stop
+ * rules (decoder.go:441-485): stop after EOT, after more than 20 repeats of one
+ * token, or when the history reaches max_len tokens (capped at n_text_ctx).
+ * The generated ids go to out_ids[0..*out_n). On a one-stream sequence past
+ * position 0 the whole loop runs in one persistent cooperative kernel. */
+int wh_seq_generate(wh_seq *s, int32_t n, float temperature, int32_t suppress_nst, float no_speech_thold,
+                    int32_t max_len, int32_t *out_ids, int32_t *out_n);
+
+/* *out = 1 when the persistent kernel serves this sequence's greedy steps past
+ * position 0 (one stream, head size 64, every matrix of one quantised type,
+ * reference attention mode, WHISPER_HIP_PERSISTENT not 0 at creation), else 0;
+ * *launches = persistent launches made so far. No counterpart in the
+ * reference: it lets callers and tests see which path ran. */
+int wh_seq_persistent(wh_seq *s, int32_t *out, int64_t *launches);
+
 /* Per-kernel timing of the step calls: with profiling enabled every launch on
  * the sequence's stream is bracketed by a HIP event pair and accumulated per
  * kernel class ("gemv", "cross_attn", "layernorm", ...), with the launch's

@@ -33,7 +33,10 @@ int seq_step_topk(wh_seq *s, const int32_t *active, int32_t k, float temperature
                   float *out_logits);
 void seq_destroy(wh_seq *s);
 int seq_set_profiling(wh_seq *s, int32_t enable);
+int seq_generate(wh_seq *s, int32_t n, float temperature, int32_t suppress_nst, float nst, int32_t max_len,
+                 int32_t *out_ids, int32_t *out_n);
 int seq_profile_count(wh_seq *s, int32_t *n);
+int seq_persistent(wh_seq *s, int32_t *out, int64_t *launches);
 int seq_profile_get(wh_seq *s, int32_t i, char *name, int32_t cap, double *ms, int64_t *launches, double *bytes);
 int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, int32_t enc_len, int32_t enc_dim,
                         const wh_decode_params *params, int32_t *out_tokens, int32_t cap, int32_t *out_lens,
@@ -368,6 +371,11 @@ int wh_seq_step_topk(wh_seq *s, const int32_t *active, int32_t k, float temperat
     if (!out_tok || !out_logprob) return fail(WH_ERR_INVALID, "seq: null output");
     return seq_step_topk(s, active, k, temperature, out_tok, out_logprob, out_logits);
 }
+int wh_seq_generate(wh_seq *s, int32_t n, float temperature, int32_t suppress_nst, float nst, int32_t max_len,
+                    int32_t *out_ids, int32_t *out_n) {
+    return seq_generate(s, n, temperature, suppress_nst, nst, max_len, out_ids, out_n);
+}
+int wh_seq_persistent(wh_seq *s, int32_t *out, int64_t *launches) { return seq_persistent(s, out, launches); }
 int wh_seq_set_profiling(wh_seq *s, int32_t enable) { return seq_set_profiling(s, enable); }
 int wh_seq_profile_count(wh_seq *s, int32_t *n) { return seq_profile_count(s, n); }
 int wh_seq_profile_get(wh_seq *s, int32_t i, char *name, int32_t cap, double *ms, int64_t *launches, double *bytes) {

@@ -65,7 +65,13 @@ void devmat_free(DevMat &m);
 struct Layer {
     float *ln1w, *ln1b, *sqb, *svb, *sob, *ln2w, *ln2b, *cqb, *cvb, *cob, *ln3w, *ln3b, *fc1b, *fc2b;
     DevMat sq, sk, sv, so, cq, ck, cv, co, fc1, fc2;
+    // q, k, v stacked as one [3d, d] matrix when they share a quantised type;
+    // sq/sk/sv are then views into its planes (alloc == nullptr)
+    DevMat sqkv;
 };
+// Stack same-type matrices with equal column counts into one allocation; the
+// parts become views into it.
+int devmat_stack(std::vector<DevMat *> parts, DevMat &out);
 
 }  // namespace wh
 

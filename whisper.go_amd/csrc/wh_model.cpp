@@ -146,7 +146,7 @@ void model_free(wh_model *m) {
     if (!m) return;
     devmat_free(m->tok);
     for (auto &l : m->layers) {
-        DevMat *ms[] = {&l.sq, &l.sk, &l.sv, &l.so, &l.cq, &l.ck, &l.cv, &l.co, &l.fc1, &l.fc2};
+        DevMat *ms[] = {&l.sq, &l.sk, &l.sv, &l.so, &l.cq, &l.ck, &l.cv, &l.co, &l.fc1, &l.fc2, &l.sqkv};
         for (DevMat *d : ms) devmat_free(*d);
     }
     if (m->vec_alloc) (void)hipFree(m->vec_alloc);
@@ -267,6 +267,8 @@ int model_create(const wh_tensor *tensors, int32_t n, const wh_meta *meta, int32
             {"mlp.0.weight", &l.fc1, 4 * d, d},       {"mlp.2.weight", &l.fc2, d, 4 * d}};
         for (auto &mm : mats)
             if ((rc = load_matrix(tab, p + mm.suf, mm.rows, mm.cols, *mm.mat))) return rc;
+        if (is_quant_type(l.sq.type) && l.sq.type == l.sk.type && l.sk.type == l.sv.type)
+            if ((rc = devmat_stack({&l.sq, &l.sk, &l.sv}, l.sqkv))) return rc;
     }
     if ((rc = load_vector(tab, "decoder.ln.weight", arena, &m->lnw, (size_t)d))) return rc;
     if ((rc = load_vector(tab, "decoder.ln.bias", arena, &m->lnb, (size_t)d))) return rc;

@@ -343,6 +343,54 @@ int devmat_upload_typed(DevMat &m, uint32_t src_type, const uint8_t *raw, uint64
     return WH_OK;
 }
 
+int devmat_stack(std::vector<DevMat *> parts, DevMat &out) {
+    if (parts.empty()) return fail(WH_ERR_INVALID, "stack: no matrices");
+    const uint32_t type = parts[0]->type;
+    const int32_t cols = parts[0]->cols;
+    int32_t rows = 0;
+    for (DevMat *p : parts) {
+        if (p->type != type || p->cols != cols || !p->alloc) return fail(WH_ERR_INVALID, "stack: incompatible matrices");
+        rows += p->rows;
+    }
+    DevMat m;
+    int rc = devmat_plan(m, type, rows, cols);
+    if (rc) return rc;
+    const Plan pl = plan_of(type, rows, m.nb);
+    void *d = nullptr;
+    WH_HIP(hipMalloc(&d, pl.total));
+    const uint64_t qs_row = pl.qs_bytes / (uint64_t)rows, sc_row = pl.sc_bytes / (uint64_t)rows,
+                   qh_row = pl.qh_bytes / (uint64_t)rows;
+    uint64_t r0 = 0;
+    for (DevMat *p : parts) {
+        const uint64_t n = (uint64_t)p->rows;
+        hipError_t e = hipMemcpy((uint8_t *)d + r0 * qs_row, p->qs, n * qs_row, hipMemcpyDeviceToDevice);
+        if (e == hipSuccess && sc_row)
+            e = hipMemcpy((uint8_t *)d + pl.sc_off + r0 * sc_row, p->sc, n * sc_row, hipMemcpyDeviceToDevice);
+        if (e == hipSuccess && qh_row)
+            e = hipMemcpy((uint8_t *)d + pl.qh_off + r0 * qh_row, p->qh, n * qh_row, hipMemcpyDeviceToDevice);
+        if (e != hipSuccess) {
+            (void)hipFree(d);
+            return fail(WH_ERR_HIP, std::string("hip: stack copy: ") + hipGetErrorString(e));
+        }
+        r0 += n;
+    }
+    m.alloc = d;
+    m.qs = d;
+    m.sc = pl.sc_bytes ? (void *)((uint8_t *)d + pl.sc_off) : nullptr;
+    m.qh = pl.qh_bytes ? (uint32_t *)((uint8_t *)d + pl.qh_off) : nullptr;
+    m.dev_bytes = pl.total;
+    r0 = 0;
+    for (DevMat *p : parts) {
+        devmat_free(*p);
+        p->qs = (uint8_t *)d + r0 * qs_row;
+        p->sc = sc_row ? (void *)((uint8_t *)m.sc + r0 * sc_row) : nullptr;
+        p->qh = qh_row ? (uint32_t *)((uint8_t *)m.qh + r0 * qh_row) : nullptr;
+        r0 += (uint64_t)p->rows;
+    }
+    out = m;
+    return WH_OK;
+}
+
 void devmat_free(DevMat &m) {
     if (m.alloc) (void)hipFree(m.alloc);
     m.alloc = m.qs = m.sc = nullptr;

@@ -11,8 +11,12 @@
 #include <vector>
 
 #include "wh_internal.h"
+#include "wh_mega.h"
 
 namespace wh {
+namespace mega {
+int launch_decode(uint32_t type, int grid, const MegaArgs &a, hipStream_t st);
+}
 
 __global__ void k_zero_rows(float *base, size_t stride, int count, int len) {
     for (int r = blockIdx.x; r < count; r += gridDim.x)
@@ -39,7 +43,17 @@ struct wh_seq {
     float *topk_lp = nullptr, *topk_logz = nullptr;
     std::vector<int32_t> h_len;     // host mirror of hist_len
     std::vector<int32_t> h_active;  // host mirror of active
+    std::vector<std::vector<int32_t>> h_hist;  // host mirror of the histories
     int32_t *pinned_ids = nullptr;
+
+    // persistent decode kernel (one stream, reference mask, uniform weight type)
+    bool mega_ok = false;
+    int mega_grid = 0;
+    uint32_t mega_type = 0;
+    unsigned mega_g = 0;
+    int64_t mega_launches = 0;
+    wh::mega::MegaArgs mega{};
+    int32_t *mega_state = nullptr;  // pinned host copy of state_out
 
     // optional per-kernel timing: an event pair around every launch
     struct ProfCat {
@@ -89,6 +103,7 @@ struct wh_seq {
         for (hipEvent_t e : ev_pool) (void)hipEventDestroy(e);
         for (void *p : allocs) (void)hipFree(p);
         if (pinned_ids) (void)hipHostFree(pinned_ids);
+        if (mega_state) (void)hipHostFree(mega_state);
         if (st) (void)hipStreamDestroy(st);
     }
     template <typename T>
@@ -223,6 +238,203 @@ int check_positions(const wh_seq &s) {
     return WH_OK;
 }
 
+MatView view(const DevMat &m) {
+    MatView v;
+    v.qs = (const uint8_t *)m.qs;
+    v.sc = m.sc;
+    v.qh = m.qh;
+    v.rows = m.rows;
+    v.cols = m.cols;
+    v.nb = m.nb;
+    return v;
+}
+
+int env_int(const char *name, int dflt) {
+    const char *v = getenv(name);
+    return (v && *v) ? atoi(v) : dflt;
+}
+
+// Set up the persistent decode kernel for a one-stream sequence when the model
+// fits its shape limits; otherwise the multi-kernel path serves every step.
+int mega_setup(wh_seq &s) {
+    const wh_model &m = *s.m;
+    s.mega_ok = false;
+    if (s.S != 1 || !env_int("WHISPER_HIP_PERSISTENT", 1)) return WH_OK;
+    const int d = m.n_state, H = m.n_head, L = m.n_layer;
+    if (d / H != 64 || d % 64 != 0 || d > 64 * 3 * 32 / 4 || !is_quant_type(m.tok.type)) return WH_OK;
+    for (const Layer &l : m.layers) {
+        if (!l.sqkv.alloc) return WH_OK;  // q, k, v not stacked (mixed types)
+        const DevMat *ms[] = {&l.sqkv, &l.so, &l.cq, &l.co, &l.fc1, &l.fc2};
+        for (const DevMat *x : ms)
+            if (x->type != m.tok.type) return WH_OK;
+    }
+    int dev_cus = 0, lds_max = 0;
+    if (hipDeviceGetAttribute(&dev_cus, hipDeviceAttributeMultiprocessorCount, m.device) != hipSuccess) return WH_OK;
+    if (hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, m.device) != hipSuccess)
+        return WH_OK;
+    const int W = std::min(env_int("WHISPER_HIP_GRID", dev_cus), dev_cus);
+    const int chunk = 32 * mega::PKV;
+    const int C = (s.enc_len + chunk - 1) / chunk;
+    const int items = H * C;
+    // per-workgroup row capacities of the kernel's register slots
+    auto per = [&](int rows, int n) { return (rows + n - 1) / n; };
+    const int NW = mega::WAVES;
+    if (W < 8 || items > W || W > 512 || per(d, W) > NW * mega::SD || per(4 * d, W) > NW * mega::SE) return WH_OK;
+    if (mega::lds_bytes(d, L, m.n_vocab, W) + 64 > (size_t)lds_max) return WH_OK;
+    auto fits32 = [](const DevMat &x) { return (uint64_t)x.rows * x.nb * 32 < (1ull << 32); };
+    if (!fits32(m.tok)) return WH_OK;
+    for (const Layer &l : m.layers)
+        if (!fits32(l.sqkv) || !fits32(l.so) || !fits32(l.cq) || !fits32(l.co) || !fits32(l.fc1) || !fits32(l.fc2))
+            return WH_OK;
+    // Roles. Workgroup w runs on XCD w % 8; the chunks of one head go to one
+    // XCD when they fit, so the head's redundant cross-query rows hit that
+    // XCD's L2. Side rows go to the workgroups without an item when they are
+    // enough, otherwise to every workgroup.
+    std::vector<mega::Role> roles(W);
+    for (auto &r : roles) r = mega::Role{-1, 0, 0, 0, 0, {0, 0, 0}};
+    {
+        std::vector<std::vector<int>> free_on(8);
+        for (int w = 0; w < W; w++) free_on[w % 8].push_back(w);
+        std::vector<size_t> used(8, 0);
+        bool ok = true;
+        for (int h = 0; h < H && ok; h++) {
+            int x = h % 8;
+            for (int k = 0; k < 8 && used[x] + C > free_on[x].size(); k++) x = (x + 1) % 8;
+            if (used[x] + C > free_on[x].size()) ok = false;
+            for (int c = 0; ok && c < C; c++) roles[free_on[x][used[x]++]].item = h * C + c;
+        }
+        if (!ok) {
+            for (auto &r : roles) r.item = -1;
+            for (int i = 0; i < items; i++) roles[i].item = i;
+        }
+    }
+    std::vector<int> side;
+    for (int w = 0; w < W; w++)
+        if (roles[w].item < 0) side.push_back(w);
+    const int ns = (int)side.size();
+    if (ns == 0 || per(3 * d, ns) > NW * mega::SQ || per(d, ns) > NW * mega::SO) {
+        side.clear();
+        for (int w = 0; w < W; w++) side.push_back(w);
+    }
+    if (per(3 * d, (int)side.size()) > NW * mega::SQ || per(d, (int)side.size()) > NW * mega::SO) return WH_OK;
+    for (size_t j = 0; j < side.size(); j++) {
+        const long n = (long)side.size();
+        mega::Role &r = roles[side[j]];
+        r.q0 = (int)(3L * d * j / n); r.q1 = (int)(3L * d * (j + 1) / n);
+        r.o0 = (int)((long)d * j / n); r.o1 = (int)((long)d * (j + 1) / n);
+    }
+    mega::MegaArgs &a = s.mega;
+    std::vector<mega::MegaLayer> ly(L);
+    for (int li = 0; li < L; li++) {
+        const Layer &l = m.layers[li];
+        mega::MegaLayer &x = ly[li];
+        x.sqkv = view(l.sqkv); x.so = view(l.so); x.cq = view(l.cq); x.co = view(l.co); x.fc1 = view(l.fc1);
+        x.fc2 = view(l.fc2);
+        x.ln1w = l.ln1w; x.ln1b = l.ln1b; x.svb = l.svb; x.sob = l.sob; x.ln2w = l.ln2w; x.ln2b = l.ln2b;
+        x.cqb = l.cqb; x.cob = l.cob; x.ln3w = l.ln3w; x.ln3b = l.ln3b; x.fc1b = l.fc1b; x.fc2b = l.fc2b;
+        x.crossK = s.crossK + (size_t)li * s.enc_len * d;
+        x.crossV = s.crossV + (size_t)li * s.enc_len * d;
+        x.kv = s.kv + (size_t)li * s.kv_layer;
+    }
+    int rc;
+    mega::MegaLayer *dl = nullptr;
+    if ((rc = s.alloc(&dl, (size_t)L))) return rc;
+    WH_HIP(hipMemcpy(dl, ly.data(), sizeof(mega::MegaLayer) * L, hipMemcpyHostToDevice));
+    a.layers = dl;
+    mega::Role *droles = nullptr;
+    if ((rc = s.alloc(&droles, (size_t)W))) return rc;
+    WH_HIP(hipMemcpy(droles, roles.data(), sizeof(mega::Role) * W, hipMemcpyHostToDevice));
+    a.roles = droles;
+    a.L = L; a.d = d; a.H = H; a.ctx = m.n_ctx; a.V = m.n_vocab; a.enc_len = s.enc_len;
+    a.C = C; a.chunk_len = chunk;
+    a.scale = (float)(1.0 / sqrt(64.0));
+    a.tok = view(m.tok);
+    a.pos_emb = m.pos; a.lnw = m.lnw; a.lnb = m.lnb;
+    a.hist = s.hist;
+    const int FS = mega::FLAG_STRIDE;
+#define MALLOC(p, n) do { if ((rc = s.alloc(&(p), (n)))) return rc; } while (0)
+    MALLOC(a.xg, (size_t)d); MALLOC(a.sa, (size_t)2 * d); MALLOC(a.x2, (size_t)d); MALLOC(a.hbuf, (size_t)4 * d);
+    MALLOC(a.attn, (size_t)d); MALLOC(a.cmax, (size_t)items); MALLOC(a.parts, (size_t)items * 65);
+    MALLOC(a.pval, (size_t)2 * W); MALLOC(a.pidx, (size_t)2 * W); MALLOC(a.eot_logit, 1);
+    // workgroup flags [W] then item flags [items]
+    MALLOC(a.flags, (size_t)(W + items) * FS); MALLOC(a.hflags, (size_t)H * FS);
+    MALLOC(a.hcount, (size_t)L * H * FS);
+    MALLOC(a.err, 1); MALLOC(a.state_out, 4); MALLOC(a.out_tokens, (size_t)s.hist_cap);
+#undef MALLOC
+    WH_HIP(hipMemsetAsync(a.flags, 0, sizeof(unsigned) * (W + items) * FS, s.st));
+    WH_HIP(hipMemsetAsync(a.hflags, 0, sizeof(unsigned) * H * FS, s.st));
+    WH_HIP(hipMemsetAsync(a.hcount, 0, sizeof(unsigned) * L * H * FS, s.st));
+    WH_HIP(hipMemsetAsync(a.err, 0, sizeof(unsigned), s.st));
+    WH_HIP(hipHostMalloc((void **)&s.mega_state, sizeof(int32_t) * 8, hipHostMallocDefault));
+    WH_HIP(hipStreamSynchronize(s.st));
+    s.mega_g = 0;
+    s.mega_grid = W;
+    s.mega_type = m.tok.type;
+    s.mega_ok = true;
+    return WH_OK;
+}
+
+// Run up to n greedy steps of stream 0 in the persistent kernel. Stops early on
+// the reference's rules when stop_rules is set (EOT, > 20 repeats, max_len).
+int mega_run(wh_seq &s, int n, float inv_temp, int suppress_nst, float nst, int max_len, int prev, int streak,
+             float *out_logits, int32_t *out_ids, int *produced, int *prev_out, int *streak_out) {
+    mega::MegaArgs a = s.mega;
+    const std::vector<int32_t> &h = s.h_hist[0];
+    a.tok0 = h.back();
+    a.len0 = (int)h.size();
+    a.prev0 = prev;
+    a.streak0 = streak;
+    a.n_steps = n;
+    a.max_len = max_len;
+    a.eot = s.m->eot;
+    a.suppress_nst = suppress_nst;
+    a.inv_temp = inv_temp;
+    a.nst = nst;
+    a.out_logits = out_logits ? s.logits : nullptr;
+    a.g0 = s.mega_g;
+    int rc;
+    {
+        Prof p(s, "decode_persistent", 0);  // algorithmic bytes set below, once the step count is known
+        if ((rc = mega::launch_decode(s.mega_type, s.mega_grid, a, s.st))) return rc;
+    }
+    s.mega_launches++;
+    WH_HIP(hipMemcpyAsync(s.mega_state, a.state_out, sizeof(int32_t) * 4, hipMemcpyDeviceToHost, s.st));
+    WH_HIP(hipMemcpyAsync(s.mega_state + 4, a.err, sizeof(unsigned), hipMemcpyDeviceToHost, s.st));
+    WH_HIP(hipStreamSynchronize(s.st));
+    if (s.mega_state[4] != 0) {
+        // a bounded wait expired: reset the exchange state and disable the path
+        s.mega_ok = false;
+        (void)hipMemsetAsync(a.flags, 0, sizeof(unsigned) * s.mega_grid * mega::FLAG_STRIDE, s.st);
+        (void)hipMemsetAsync(a.err, 0, sizeof(unsigned), s.st);
+        (void)hipStreamSynchronize(s.st);
+        return fail(WH_ERR_HIP, "persistent decode: a workgroup wait timed out");
+    }
+    const int got = s.mega_state[0];
+    s.mega_g = (unsigned)s.mega_state[3];
+    if (s.prof && !s.pending.empty()) {
+        // quantised weight bytes of every step the launch ran (token rows included)
+        s.pending.back().bytes = (double)s.m->weight_bytes * got;
+        s.prof_resolve();
+    }
+    std::vector<int32_t> ids(std::max(got, 1));
+    if (got > 0) WH_HIP(hipMemcpy(ids.data(), a.out_tokens, sizeof(int32_t) * got, hipMemcpyDeviceToHost));
+    if (out_logits) WH_HIP(hipMemcpy(out_logits, s.logits, sizeof(float) * s.m->n_vocab, hipMemcpyDeviceToHost));
+    for (int i = 0; i < got; i++) {
+        s.h_hist[0].push_back(ids[i]);
+        if (out_ids) out_ids[i] = ids[i];
+    }
+    s.h_len[0] = (int32_t)s.h_hist[0].size();
+    // keep the multi-kernel path's device scalars in step
+    int32_t meta[3] = {s.h_len[0], s.h_hist[0].back(), s.h_len[0] - 1};
+    WH_HIP(hipMemcpy(s.hist_len, &meta[0], 4, hipMemcpyHostToDevice));
+    WH_HIP(hipMemcpy(s.tok, &meta[1], 4, hipMemcpyHostToDevice));
+    WH_HIP(hipMemcpy(s.pos, &meta[2], 4, hipMemcpyHostToDevice));
+    *produced = got;
+    if (prev_out) *prev_out = s.mega_state[1];
+    if (streak_out) *streak_out = s.mega_state[2];
+    return WH_OK;
+}
+
 int upload_active(wh_seq &s, const int32_t *active) {
     for (int i = 0; i < s.S; i++) s.h_active[i] = active ? (active[i] != 0) : 1;
     WH_HIP(hipMemcpyAsync(s.active, s.h_active.data(), sizeof(int32_t) * s.S, hipMemcpyHostToDevice, s.st));
@@ -308,6 +520,7 @@ int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t e
     WH_HIP(hipHostMalloc((void **)&s->pinned_ids, sizeof(int32_t) * (16 * 8 * 2 + 16), hipHostMallocDefault));
     s->h_len.assign(S, 0);
     s->h_active.assign(S, 1);
+    s->h_hist.assign(S, {});
     // cross K/V projections of every encoder output (decoder.go:923-940), once per sequence
     float *enc = nullptr;
     WH_HIP(hipMalloc(&enc, sizeof(float) * (size_t)enc_len * d));
@@ -330,6 +543,7 @@ int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t e
     }
     (void)hipFree(enc);
     WH_HIP(hipStreamSynchronize(s->st));
+    if ((rc = mega_setup(*s))) return rc;
     *out = s.release();
     return WH_OK;
 }
@@ -365,7 +579,16 @@ int seq_set_tokens(wh_seq *s, int32_t i, const int32_t *tokens, int32_t n, int32
     }
     WH_HIP(hipStreamSynchronize(s->st));
     s->h_len[i] = n;
+    s->h_hist[i].assign(tokens, tokens + n);
     return WH_OK;
+}
+
+// The persistent kernel serves a step of a one-stream sequence past position 0
+// (at position 0 the step writes the cache row that the same step attends).
+static bool mega_eligible(const wh_seq *s, const int32_t *active) {
+    // the persistent kernel implements the reference mask only (attention mode 0)
+    return s->mega_ok && s->S == 1 && s->m->attn_mode == 0 && (!active || active[0]) && s->h_len[0] >= 2 &&
+           s->h_len[0] - 1 < s->m->n_ctx && s->h_len[0] + 1 <= s->hist_cap;
 }
 
 static int seq_forward_active(wh_seq *s, const int32_t *active) {
@@ -380,8 +603,15 @@ int seq_step_greedy(wh_seq *s, const int32_t *active, float temperature, int32_t
     if (!s) return fail(WH_ERR_INVALID, "seq: null handle");
     WH_HIP(hipSetDevice(s->m->device));
     int rc;
-    if ((rc = seq_forward_active(s, active))) return rc;
     const float inv = temperature > 0 ? 1.0f / temperature : 1.0f;
+    if (mega_eligible(s, active)) {
+        int got = 0;
+        if ((rc = mega_run(*s, 1, inv, suppress_nst, nst, s->hist_cap, -1, 0, out_logits, out_ids, &got, nullptr,
+                           nullptr)))
+            return rc;
+        return WH_OK;
+    }
+    if ((rc = seq_forward_active(s, active))) return rc;
     const int V = s->m->n_vocab;
     {
         Prof p(*s, "sample", 0);
@@ -399,9 +629,58 @@ int seq_step_greedy(wh_seq *s, const int32_t *active, float temperature, int32_t
     if (s->prof) s->prof_resolve();
     for (int i = 0; i < s->S; i++) {
         if (out_ids) out_ids[i] = s->h_active[i] ? s->pinned_ids[i] : -1;
-        if (s->h_active[i]) s->h_len[i]++;
+        if (s->h_active[i]) {
+            s->h_len[i]++;
+            s->h_hist[i].push_back(s->pinned_ids[i]);
+        }
     }
     return WH_OK;
+}
+
+// Up to n greedy steps of stream 0 with the reference's stop rules
+// (decoder.go:441-485): EOT, more than 20 repeats of one token, max_len
+// tokens. Returns the generated ids; the persistent kernel runs them on the
+// device when it serves the sequence, else one multi-kernel step per token.
+static int generate_impl(wh_seq *s, int32_t n, float temperature, int32_t suppress_nst, float nst, int32_t max_len,
+                         int32_t *out_ids, int32_t *out_n, int &prev, int &streak) {
+    *out_n = 0;
+    if (s->h_len[0] == 0) return fail(WH_ERR_INVALID, "model: decode: forward: no tokens in state");
+    WH_HIP(hipSetDevice(s->m->device));
+    const float inv = temperature > 0 ? 1.0f / temperature : 1.0f;
+    if (max_len > s->m->n_ctx) max_len = s->m->n_ctx;  // the reference caps at n_text_ctx
+    int rc;
+    int produced = 0;
+    while (produced < n && s->h_len[0] < max_len) {
+        int32_t id;
+        if (mega_eligible(s, nullptr)) {
+            int got = 0;
+            if ((rc = mega_run(*s, n - produced, inv, suppress_nst, nst, max_len, prev, streak, nullptr,
+                               out_ids ? out_ids + produced : nullptr, &got, &prev, &streak)))
+                return rc;
+            produced += got;
+            *out_n = produced;
+            const int32_t last = s->h_hist[0].back();
+            if (got == 0 || last == s->m->eot || streak > 20) break;
+            continue;
+        }
+        if ((rc = seq_step_greedy(s, nullptr, temperature, suppress_nst, nst, &id, nullptr))) return rc;
+        if (out_ids) out_ids[produced] = id;
+        produced++;
+        *out_n = produced;
+        if (id == s->m->eot) break;
+        if (prev == id) streak++;
+        else { streak = 1; prev = id; }
+        if (streak > 20) break;
+    }
+    return WH_OK;
+}
+
+int seq_generate(wh_seq *s, int32_t n, float temperature, int32_t suppress_nst, float nst, int32_t max_len,
+                 int32_t *out_ids, int32_t *out_n) {
+    if (!s || !out_n) return fail(WH_ERR_INVALID, "seq: null argument");
+    if (s->S != 1) return fail(WH_ERR_INVALID, "seq: generate needs a one-stream sequence");
+    int prev = -1, streak = 0;
+    return generate_impl(s, n, temperature, suppress_nst, nst, max_len, out_ids, out_n, prev, streak);
 }
 
 int seq_step_topk(wh_seq *s, const int32_t *active, int32_t k, float temperature, int32_t *out_tok, float *out_lp,
@@ -510,6 +789,13 @@ int seq_profile_get(wh_seq *s, int32_t i, char *name, int32_t cap, double *ms, i
     return WH_OK;
 }
 
+int seq_persistent(wh_seq *s, int32_t *out, int64_t *launches) {
+    if (!s || !out) return fail(WH_ERR_INVALID, "seq: null argument");
+    *out = s->mega_ok && s->m->attn_mode == 0;
+    if (launches) *launches = s->mega_launches;
+    return WH_OK;
+}
+
 int seq_profile_count(wh_seq *s, int32_t *n) {
     if (!s || !n) return fail(WH_ERR_INVALID, "seq: null argument");
     *n = (int32_t)s->prof_cats.size();
@@ -565,6 +851,22 @@ int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, 
     // one temperature / suppress setting per call: streams share the first params
     const wh_decode_params &p0 = params[0];
     const float base = p0.temperature == 0 ? 1.0f : p0.temperature;
+    if (S == 1 && active[0]) {
+        // the token loop runs on the device in chunks; cancellation is polled between chunks
+        constexpr int CHUNK = 32;
+        const int max_len = p0.prompt_len + maxt[0];
+        std::vector<int32_t> got(CHUNK);
+        int pv = -1, st = 0;
+        while (active[0]) {
+            if (cancelled(cancel)) return fail(WH_ERR_CANCELLED, "model: decode: cancelled: context canceled");
+            int32_t n = 0;
+            if ((rc = generate_impl(s.get(), CHUNK, base, p0.suppress_nst, p0.no_speech_thold, max_len, got.data(), &n,
+                                    pv, st)))
+                return fail(rc, std::string("model: decode: forward: ") + wh_last_error());
+            toks[0].insert(toks[0].end(), got.begin(), got.begin() + n);
+            if (n < CHUNK || toks[0].back() == m->eot || st > 20 || (int)toks[0].size() >= max_len) active[0] = 0;
+        }
+    }
     while (std::any_of(active.begin(), active.end(), [](int32_t a) { return a != 0; })) {
         if (cancelled(cancel)) return fail(WH_ERR_CANCELLED, "model: decode: cancelled: context canceled");
         if ((rc = seq_step_greedy(s.get(), active.data(), base, p0.suppress_nst, p0.no_speech_thold, ids.data(), nullptr)))

@@ -257,6 +257,24 @@ class Sequence:
             _raise(rc)
         return (list(ids), out) if logits else list(ids)
 
+    def generate(self, n, temperature=1.0, suppress_nst=False, no_speech_thold=0.0, max_len=None):
+        """Up to n greedy steps of stream 0 with the reference's stop rules."""
+        ids = (C.c_int32 * max(1, n))()
+        got = C.c_int32()
+        ml = self.dec.n_ctx if max_len is None else int(max_len)
+        rc = lib().wh_seq_generate(self._h, int(n), float(temperature), int(bool(suppress_nst)),
+                                   float(no_speech_thold), ml, ids, C.byref(got))
+        if rc != native.WH_OK:
+            _raise(rc)
+        return list(ids[:got.value])
+
+    @property
+    def persistent(self):
+        """(served by the persistent kernel, persistent launches so far)."""
+        on, n = C.c_int32(), C.c_int64()
+        check(lib().wh_seq_persistent(self._h, C.byref(on), C.byref(n)))
+        return bool(on.value), n.value
+
     def set_profiling(self, enable):
         check(lib().wh_seq_set_profiling(self._h, int(bool(enable))))
 

@@ -88,6 +88,9 @@ _SIGS = [
                                      C.POINTER(C.c_int32), _P]),
     ("wh_seq_step_topk", C.c_int, [_P, C.POINTER(C.c_int32), C.c_int32, C.c_float, C.POINTER(C.c_int32),
                                    C.POINTER(C.c_float), _P]),
+    ("wh_seq_generate", C.c_int, [_P, C.c_int32, C.c_float, C.c_int32, C.c_float, C.c_int32,
+                                  C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
+    ("wh_seq_persistent", C.c_int, [_P, C.POINTER(C.c_int32), C.POINTER(C.c_int64)]),
     ("wh_seq_set_profiling", C.c_int, [_P, C.c_int32]),
     ("wh_seq_profile_count", C.c_int, [_P, C.POINTER(C.c_int32)]),
     ("wh_seq_profile_get", C.c_int, [_P, C.c_int32, C.c_char_p, C.c_int32, C.POINTER(C.c_double),
