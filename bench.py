@@ -76,10 +76,24 @@ def generate_n(seq, n):
     return out
 
 
+def copy_calibration(wh, mib):
+    """Device-to-device copies of a known size: their FETCH_SIZE / WRITE_SIZE in
+    a rocprofv3 --pmc run give the scale factor for the decode kernel's counters."""
+    n = mib << 20
+    src, dst = wh.native.DevBuf(n), wh.native.DevBuf(n)
+    for _ in range(2):
+        wh.native.check(wh.native.lib().wh_memcpy(dst.ptr, src.ptr, n, 2))
+    log(f"bench: copy calibration: 2 x {n} bytes device to device")
+    src.free()
+    dst.free()
+
+
 def run_decode(args):
     wh = __graft_entry__.load_package()
     if wh.native.device_count() < 1:
         raise SystemExit("bench: no GPU visible")
+    if args.copy_mib > 0:
+        copy_calibration(wh, args.copy_mib)
     qtype = QNAMES[args.qtype]
     t0 = time.time()
     tensors, meta = wh.synth.make_decoder(args.config, qtype)
@@ -215,6 +229,8 @@ def main():
     ap.add_argument("--multikernel-steps", type=int, default=32,
                     help="also time this many steps with one launch per kernel (0 = skip)")
     ap.add_argument("--cpu-tokens", type=int, default=3, help="oracle steps timed for cpu_baseline (0 = skip)")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="first copy this many MiB device to device (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--gemv", action="store_true", help="run the standalone GEMV microbench instead")
     ap.add_argument("--gemv-formats", default="Q8_0,Q4_0,Q4_1,Q5_0,Q5_1")
     args = ap.parse_args()

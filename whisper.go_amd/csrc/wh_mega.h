@@ -55,11 +55,13 @@ constexpr int WAVES = THREADS / 64;
 constexpr int FLAG_STRIDE = 16;
 constexpr int PKV = 8;      // float4 of K (and of V) per thread: 256-key chunks
 constexpr int PFC2 = 3;     // fc2 input passes: n_state <= 64*3*32/4 = 1536
-constexpr int SQ = 4;       // q,k,v side rows per wave
-constexpr int SO = 2;       // self-attention output side rows per wave
-constexpr int SD = 2;       // cross output rows per wave (also fc2 rows)
-constexpr int SE = 5;       // fc1 rows per wave
-constexpr int TS = 6;       // logits rows per wave per chunk
+// register slots (rows) per wave: a workgroup holds WAVES * slots rows of each kind
+constexpr int SCQ = 8;      // cross query rows of one head: 64 = 8 * 8
+constexpr int SQ = 4;       // q,k,v side rows
+constexpr int SO = 2;       // self-attention output side rows
+constexpr int SD = 2;       // cross output rows (also fc2 rows)
+constexpr int SE = 5;       // fc1 rows
+constexpr int TS = 6;       // logits rows per chunk
 
 // Dynamic LDS bytes of the kernel for n_state d, L layers, V vocabulary rows
 // and a grid of W workgroups.

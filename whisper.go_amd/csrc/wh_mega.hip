@@ -50,6 +50,7 @@ namespace mega {
 
 constexpr int NT = THREADS;
 constexpr int NW = WAVES;
+constexpr int NC = NW;  // waves holding weight rows (all: more loads in flight beat a load-free poller)
 constexpr int FS = FLAG_STRIDE;
 constexpr unsigned SPIN_MAX = 1u << 22;
 
@@ -97,6 +98,9 @@ __device__ __forceinline__ int tid() {
 
 // A value that is the same on every lane, kept in a scalar register.
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Index of this wave among the NC waves holding weight rows (-1: none).
+__device__ __forceinline__ int cwave() { return uni(tid() >> 6) - (NW - NC); }
 
 // A pointer that is the same on every lane, moved to scalar registers and
 // typed as global memory.
@@ -176,27 +180,57 @@ __device__ __forceinline__ void publish(unsigned *flags, int slot, unsigned g) {
 }
 
 // Wait until flags[(first + i) * FS] >= g for i < count (count <= 512).
-// Wave 0 polls; the other waves wait at the barrier.
+// Wave 0 polls with two rounds of loads in flight (the older round is tested
+// while the newer one travels); the other waves wait at the barrier.
 __device__ __forceinline__ void wait_flags(const unsigned *flags, int first, int count, unsigned g, unsigned *err) {
     const int t = tid();
     if (t < 64) {
+        unsigned v0[8], v1[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int i = t + 64 * k;
+            v0[k] = i < count ? ld_u(&flags[(unsigned)(first + i) * FS]) : 0xFFFFFFFFu;
+        }
         unsigned spins = 0;
         for (;;) {
-            bool ok = true;
 #pragma unroll
             for (int k = 0; k < 8; k++) {
                 const int i = t + 64 * k;
-                if (i < count) ok &= ld_u(&flags[(unsigned)(first + i) * FS]) >= g;
+                v1[k] = i < count ? ld_u(&flags[(unsigned)(first + i) * FS]) : 0xFFFFFFFFu;
             }
+            bool ok = true;
+#pragma unroll
+            for (int k = 0; k < 8; k++) ok &= v0[k] >= g;
             if (__all(ok)) break;
             if (++spins > SPIN_MAX || ((spins & 255) == 0 && ld_u(err))) {
                 if (t == 0) atomicOr(err, 1u);
                 break;
             }
-            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int k = 0; k < 8; k++) v0[k] = v1[k];
         }
     }
     __syncthreads();
+}
+
+// LDS vectors keep each 32-element block in 36 slots: a lane reading its whole
+// block then hits 4 banks no other lane of its 16-lane group uses.
+__device__ __forceinline__ int pad(int i) { return i + ((i >> 5) << 2); }
+
+// n floats (n even, src 8-byte aligned) of a coherent exchange vector into a
+// padded LDS vector, two per 64-bit load.
+__device__ __forceinline__ void xload_pad(float *dst, const float *src, int n) {
+    for (int i = tid(); i < n / 2; i += NT) {
+        const uint64_t v = __hip_atomic_load((const uint64_t *)src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *(float2 *)&dst[pad(2 * i)] = make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+    }
+}
+// same into a plain LDS vector
+__device__ __forceinline__ void xload(float *dst, const float *src, int n) {
+    for (int i = tid(); i < n / 2; i += NT) {
+        const uint64_t v = __hip_atomic_load((const uint64_t *)src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *(float2 *)&dst[2 * i] = make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+    }
 }
 
 // ---- weight rows prefetched into registers ----------------------------------------
@@ -232,10 +266,20 @@ __device__ __forceinline__ void load_blk(const UView &m, unsigned blk, uint4 &a,
 // ranges and spill) and no branch surrounds the loads.
 template <int TYPE, int MAXS, int PASSES>
 __device__ __forceinline__ void prefetch(Pre<TYPE, MAXS> &P, const UView &m, int nb, int r0, int r1) {
-    const int t = tid(), lane = t & 63, wave = t >> 6;
+    const int lane = tid() & 63, cw = cwave();
+    if (cw < 0) {
+#pragma unroll
+        for (int s = 0; s < MAXS; s++) {
+            P.a[s] = make_uint4(0u, 0u, 0u, 0u);
+            P.b[s] = make_uint4(0u, 0u, 0u, 0u);
+            P.s[s] = 0u;
+            P.h[s] = 0u;
+        }
+        return;
+    }
 #pragma unroll
     for (int s = 0; s < MAXS; s++) {
-        const int r = max(min(r0 + wave + NW * (s / PASSES), r1 - 1), 0);
+        const int r = max(min(r0 + cw + NC * (s / PASSES), r1 - 1), 0);
         const int b = min(lane + 64 * (s % PASSES), nb - 1);
         load_blk<TYPE>(m, (unsigned)r * (unsigned)nb + (unsigned)b, P.a[s], P.b[s], P.s[s], P.h[s]);
     }
@@ -281,10 +325,6 @@ __device__ __forceinline__ float block_dot(const uint4 &a, const uint4 &b, uint3
     }
 }
 
-// LDS vectors keep each 32-element block in 36 slots: a lane reading its whole
-// block then hits 4 banks no other lane of its 16-lane group uses.
-__device__ __forceinline__ int pad(int i) { return i + ((i >> 5) << 2); }
-
 // Activation block b of a padded LDS vector (16-byte aligned) into registers.
 __device__ __forceinline__ void lds_block(const float *xs, int b, float (&xr)[32]) {
     const float4 *x4 = (const float4 *)(xs + b * 36);
@@ -299,15 +339,17 @@ __device__ __forceinline__ void lds_block(const float *xs, int b, float (&xr)[32
 }
 
 // Row dots of the prefetched slots: out[k] (same on every lane) is the dot of
-// row r0 + wave + NW*k with the padded LDS vector xs of nb blocks. Lanes past
-// the last block and rows past r1 compute on duplicate data and add zero.
+// row r0 + cw + NC*k (cw = cwave()) with the padded LDS vector xs of nb
+// blocks. Lanes past the last block and rows past r1 compute on duplicate
+// data and add zero; the poller wave returns zeros.
 template <int TYPE, int MAXS, int PASSES>
 __device__ __forceinline__ void row_dots(const Pre<TYPE, MAXS> &P, int nb, int r0, int r1, const float *xs,
                                          float (&out)[MAXS / PASSES]) {
-    const int t = tid(), lane = t & 63, wave = t >> 6;
+    const int lane = tid() & 63, cw = cwave();
     constexpr int K = MAXS / PASSES;
 #pragma unroll
     for (int k = 0; k < K; k++) out[k] = 0.0f;
+    if (cw < 0) return;
 #pragma unroll
     for (int p = 0; p < PASSES; p++) {
         const int b = lane + 64 * p;
@@ -316,7 +358,7 @@ __device__ __forceinline__ void row_dots(const Pre<TYPE, MAXS> &P, int nb, int r
 #pragma unroll
         for (int k = 0; k < K; k++) {
             const int s = k * PASSES + p;
-            const int r = r0 + wave + NW * k;
+            const int r = r0 + cw + NC * k;
             const float v = block_dot<TYPE>(P.a[s], P.b[s], P.s[s], P.h[s], xr);
             out[k] += (r < r1 && b < nb) ? v : 0.0f;
             __builtin_amdgcn_sched_barrier(0);  // decode one block at a time: bounded register use
@@ -326,20 +368,35 @@ __device__ __forceinline__ void row_dots(const Pre<TYPE, MAXS> &P, int nb, int r
     for (int k = 0; k < K; k++) out[k] = wave_sum(out[k]);
 }
 
-// out[lane] for lane < K (the row a lane finishes in an epilogue)
+// out[lane] for lane < K (the row a lane finishes in an epilogue). out[] is
+// wave-uniform, so each value is written into its lane with v_writelane; a
+// select chain on the lane index is turned into a private (scratch) array.
 template <int K>
-__device__ __forceinline__ float pick(const float (&out)[K], int lane) {
-    float v = out[0];
+__device__ __forceinline__ float pick(const float (&out)[K], int) {
+    float v = 0.0f;
 #pragma unroll
-    for (int k = 1; k < K; k++) v = (lane == k) ? out[k] : v;
+    for (int k = 0; k < K; k++) {
+        const int s = uni(__builtin_bit_cast(int, out[k]));
+        __asm__ volatile("v_writelane_b32 %0, %1, %2" : "+v"(v) : "s"(s), "i"(k));
+    }
     return v;
 }
 
-// Per-lane bias of row r0 + wave + NW*lane (lane < K), clamped into [r0, r1).
+// Per-lane bias of row r0 + cw + NC*lane (lane < K), clamped into [r0, r1);
+// the poller wave loads nothing.
 template <int K>
 __device__ __forceinline__ float lane_bias(gf *bias, int r0, int r1) {
-    const int t = tid(), lane = t & 63, wave = t >> 6;
-    return bias[max(min(r0 + wave + NW * min(lane, K - 1), r1 - 1), 0)];
+    const int lane = tid() & 63, cw = cwave();
+    if (cw < 0) return 0.0f;
+    return bias[max(min(r0 + cw + NC * min(lane, K - 1), r1 - 1), 0)];
+}
+
+// Row finished by this lane in an epilogue (lane < K of a compute wave), or -1.
+template <int K>
+__device__ __forceinline__ int lane_row(int r0, int r1) {
+    const int lane = tid() & 63, cw = cwave();
+    const int r = r0 + cw + NC * lane;
+    return (cw >= 0 && lane < K && r < r1) ? r : -1;
 }
 
 // LayerNorm parameters of this thread's elements t, t+NT, t+2NT (n <= 3*NT).
@@ -403,18 +460,19 @@ __device__ __forceinline__ void better(float v, int i, float &bv, int &bi) {
     if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
 }
 
-// Logits rows of one chunk (<= NW*TS rows) with penalty and running argmax.
+// Logits rows of one chunk (<= NC*TS rows) with penalty and running argmax.
 // pen[r - rv0] is the window count of row r.
 template <int TYPE>
 __device__ __forceinline__ void logits_chunk(const MegaArgs &a, const Pre<TYPE, TS> &P, int nb, int base, int end,
                                              const float *xn, const int *pen, int rv0, float &bv, int &bi,
                                              float &bv2, int &bi2) {
-    const int t = tid(), lane = t & 63, wave = t >> 6;
+    const int lane = tid() & 63, cw = cwave();
     float out[TS];
     row_dots<TYPE, TS, 1>(P, nb, base, end, xn, out);
+    if (cw < 0) return;
 #pragma unroll
     for (int k = 0; k < TS; k++) {
-        const int r = base + wave + NW * k;
+        const int r = base + cw + NC * k;
         if (r < end) {
             float v = out[k];
             if (a.out_logits && lane == 0) a.out_logits[r] = v;
@@ -451,8 +509,8 @@ __device__ __forceinline__ void side_prefetch(Side<TYPE> &S, const MegaArgs &a, 
     prefetch<TYPE, SQ, 1>(S.pq, uview(Ly.sqkv), nbd, q0, q1);
     ln_load(S.p1, glob<gf>(Ly.ln1w), glob<gf>(Ly.ln1b), a.d);
     // v rows take the v bias; k rows have none; q rows are not used
-    const int t = tid(), lane = t & 63, wave = t >> 6;
-    const int r = max(min(q0 + wave + NW * min(lane, SQ - 1), q1 - 1), 0);
+    const int lane = tid() & 63, cw = max(cwave(), 0);
+    const int r = max(min(q0 + cw + NC * min(lane, SQ - 1), q1 - 1), 0);
     S.qb = glob<gf>(Ly.svb)[max(r - 2 * a.d, 0)];
     // the last layer has no next layer: its own rows are loaded and not used
     const MegaLayer &Ln = ls[min(l + 1, a.L - 1)];
@@ -466,16 +524,16 @@ template <int TYPE>
 __device__ __forceinline__ void side_compute(const Side<TYPE> &S, const MegaArgs &a, const MegaLayer *ls, int l,
                                              int q0, int q1, int o0, int o1, int nbd, int pos, const float *xs,
                                              float *xn, const float *v0, float *red) {
-    const int t = tid(), lane = t & 63, wave = t >> 6;
+    const int lane = tid() & 63;
     const int d = a.d;
     {
         layernorm(xs, xn, d, S.p1, red);
         float out[SQ];
         row_dots<TYPE, SQ, 1>(S.pq, nbd, q0, q1, xn, out);
         const float v = pick<SQ>(out, lane);
-        const int r = q0 + wave + NW * lane;
+        const int r = lane_row<SQ>(q0, q1);
         // rows [0,d) q (unused under the reference mask), [d,2d) k, [2d,3d) v
-        if (lane < SQ && r < q1 && r >= d) {
+        if (r >= d) {
             const int j = r % d, hh = j / 64, c = j % 64;
             const bool isv = r >= 2 * d;  // S.qb holds this lane's v bias then
             gfw *kv = glob<gfw>(ls[l].kv);
@@ -488,8 +546,8 @@ __device__ __forceinline__ void side_compute(const Side<TYPE> &S, const MegaArgs
         float out[SO];
         row_dots<TYPE, SO, 1>(S.po, nbd, o0, o1, v0, out);
         const float v = pick<SO>(out, lane);
-        const int r = o0 + wave + NW * lane;
-        if (lane < SO && r < o1 && l + 1 < a.L) st_f(&a.sa[(size_t)((l + 1) & 1) * d + r], v + S.ob);
+        const int r = lane_row<SO>(o0, o1);
+        if (r >= 0 && l + 1 < a.L) st_f(&a.sa[(size_t)((l + 1) & 1) * d + r], v + S.ob);
     }
 }
 
@@ -557,8 +615,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 float out[SO];
                 row_dots<TYPE, SO, 1>(po, nbd, o0, o1, v0, out);
                 const float v = pick<SO>(out, lane);
-                const int r = o0 + wave + NW * lane;
-                if (lane < SO && r < o1) st_f(&a.sa[r], v + ob);
+                const int r = lane_row<SO>(o0, o1);
+                if (r >= 0) st_f(&a.sa[r], v + ob);
             }
             TRACE(step, 0, 7, 2);
             publish(a.flags, w, ++g);
@@ -572,9 +630,9 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 const MegaLayer &Ly = ls[l];
                 if (has_item) {
                     float4 kr[PKV];
-                    Pre<TYPE, 8> pc;
+                    Pre<TYPE, SCQ> pc;
                     LnPar p2;
-                    prefetch<TYPE, 8, 1>(pc, uview(Ly.cq), nbd, ih * 64, ih * 64 + 64);
+                    prefetch<TYPE, SCQ, 1>(pc, uview(Ly.cq), nbd, ih * 64, ih * 64 + 64);
                     gf *K = glob<gf>(Ly.crossK) + (size_t)ih * a.enc_len * 64;
                     const int tt = tid();
 #pragma unroll
@@ -584,23 +642,23 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                         kr[j] = ld16f(K + (unsigned)t * 64u + 4u * (unsigned)(tt & 15));
                     }
                     ln_load(p2, glob<gf>(Ly.ln2w), glob<gf>(Ly.ln2b), d);
-                    const float qb = lane_bias<8>(glob<gf>(Ly.cqb), ih * 64, ih * 64 + 64);
+                    const float qb = lane_bias<SCQ>(glob<gf>(Ly.cqb), ih * 64, ih * 64 + 64);
                     wait_flags(a.flags, 0, W, gin, a.err);
                     TRACE(step, l, 1, 1);
-                    if (l > 0) {
-                        for (int i = tid(); i < d; i += NT) xs[pad(i)] = ld_f(&a.xg[i]);
-                    } else {
-                        for (int i = tid(); i < d; i += NT) sav[i] = ld_f(&a.sa[i]);
-                    }
+                    if (l > 0) xload_pad(xs, a.xg, d);
+                    else xload(sav, a.sa, d);
                     __syncthreads();
                     for (int i = tid(); i < d; i += NT) x1s[pad(i)] = xs[pad(i)] + sav[i];
                     __syncthreads();
                     TRACE(step, l, 1, 3);
                     layernorm(x1s, xn, d, p2, red);
                     TRACE(step, l, 1, 4);
-                    float out[8];
-                    row_dots<TYPE, 8, 1>(pc, nbd, ih * 64, ih * 64 + 64, xn, out);
-                    if (lane < 8) qh[wave + NW * lane] = pick<8>(out, lane) + qb;
+                    float out[SCQ];
+                    row_dots<TYPE, SCQ, 1>(pc, nbd, ih * 64, ih * 64 + 64, xn, out);
+                    {
+                        const int r = lane_row<SCQ>(ih * 64, ih * 64 + 64);
+                        if (r >= 0) qh[r - ih * 64] = pick<SCQ>(out, lane) + qb;
+                    }
                     __syncthreads();
                     TRACE(step, l, 1, 5);
                     const float4 q4 = ((const float4 *)qh)[tid() & 15];
@@ -631,11 +689,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                     side_prefetch<TYPE>(S, a, ls, l, q0, q1, o0, o1, nbd, v0);
                     wait_flags(a.flags, 0, W, gin, a.err);
                     TRACE(step, l, 1, 1);
-                    if (l > 0) {
-                        for (int i = tid(); i < d; i += NT) xs[pad(i)] = ld_f(&a.xg[i]);
-                    } else {
-                        for (int i = tid(); i < d; i += NT) sav[i] = ld_f(&a.sa[i]);  // for D's x1 rows
-                    }
+                    if (l > 0) xload_pad(xs, a.xg, d);
+                    else xload(sav, a.sa, d);  // for D's x1 rows
                     __syncthreads();
                     side_compute<TYPE>(S, a, ls, l, q0, q1, o0, o1, nbd, pos, xs, xn, v0, red);
                     TRACE(step, l, 1, 2);
@@ -742,14 +797,14 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 const float cb = lane_bias<SD>(glob<gf>(Ly.cob), rd0, rd1);
                 wait_flags(a.hflags, 0, H, gC, a.err);
                 TRACE(step, l, 3, 1);
-                for (int i = tid(); i < d; i += NT) xn[pad(i)] = ld_f(&a.attn[i]);
+                xload_pad(xn, a.attn, d);
                 __syncthreads();
                 {
                     float out[SD];
                     row_dots<TYPE, SD, 1>(pd, nbd, rd0, rd1, xn, out);
                     const float v = pick<SD>(out, lane);
-                    const int r = rd0 + wave + NW * lane;
-                    if (lane < SD && r < rd1) {
+                    const int r = lane_row<SD>(rd0, rd1);
+                    if (r >= 0) {
                         const float x1 = xl_own[r - rd0] + sav[r];
                         const float x2 = x1 + (v + cb);
                         x2_own[r - rd0] = x2;
@@ -772,7 +827,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 ln_load(p3, glob<gf>(Ly.ln3w), glob<gf>(Ly.ln3b), d);
                 wait_flags(a.flags, 0, W, gD, a.err);
                 TRACE(step, l, 4, 1);
-                for (int i = tid(); i < d; i += NT) xs[pad(i)] = ld_f(&a.x2[i]);
+                xload_pad(xs, a.x2, d);
                 __syncthreads();
                 TRACE(step, l, 4, 3);
                 layernorm(xs, xn, d, p3, red);
@@ -782,8 +837,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                     row_dots<TYPE, SE, 1>(pe, nbd, rf0, rf1, xn, out);
                     TRACE(step, l, 4, 5);
                     const float v = pick<SE>(out, lane);
-                    const int r = rf0 + wave + NW * lane;
-                    if (lane < SE && r < rf1) st_f(&a.hbuf[r], gelu_ref(v + fb));
+                    const int r = lane_row<SE>(rf0, rf1);
+                    if (r >= 0) st_f(&a.hbuf[r], gelu_ref(v + fb));
                 }
                 TRACE(step, l, 4, 2);
                 publish(a.flags, w, ++g);
@@ -799,11 +854,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 const float fb = lane_bias<SD>(glob<gf>(Ly.fc2b), rd0, rd1);
                 wait_flags(a.flags, 0, W, gE, a.err);
                 TRACE(step, l, 5, 1);
-                for (int i = tid(); i < 4 * d; i += NT) xn[pad(i)] = ld_f(&a.hbuf[i]);
-                if (l + 1 < L) {
-                    const float *sn = a.sa + (size_t)((l + 1) & 1) * d;
-                    for (int i = tid(); i < d; i += NT) sav[i] = ld_f(&sn[i]);
-                }
+                xload_pad(xn, a.hbuf, 4 * d);
+                if (l + 1 < L) xload(sav, a.sa + (size_t)((l + 1) & 1) * d, d);
                 __syncthreads();
                 TRACE(step, l, 5, 3);
                 {
@@ -811,8 +863,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                     row_dots<TYPE, SD * PFC2, PFC2>(pf, nbf, rd0, rd1, xn, out);
                     TRACE(step, l, 5, 5);
                     const float v = pick<SD>(out, lane);
-                    const int r = rd0 + wave + NW * lane;
-                    if (lane < SD && r < rd1) {
+                    const int r = lane_row<SD>(rd0, rd1);
+                    if (r >= 0) {
                         const float x = x2_own[r - rd0] + (v + fb);
                         xl_own[r - rd0] = x;
                         st_f(&a.xg[r], x);
@@ -829,14 +881,14 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
             TRACE(step, L, 6, 0);
             const UView vt = uview(a.tok);
             Pre<TYPE, TS> p0, p1;
-            const int CH = NW * TS;
+            const int CH = NC * TS;
             LnPar pf;
             prefetch<TYPE, TS, 1>(p0, vt, nbd, rv0, min(rv0 + CH, rv1));
             ln_load(pf, glob<gf>(a.lnw), glob<gf>(a.lnb), d);
             for (int i = tid(); i < rv1 - rv0; i += NT) pen[i] = 0;
             wait_flags(a.flags, 0, W, gF, a.err);
             TRACE(step, L, 6, 1);
-            for (int i = tid(); i < d; i += NT) xs[pad(i)] = ld_f(&a.xg[i]);
+            xload_pad(xs, a.xg, d);
             // repetition window (decoder.go:1000-1016): counts of this workgroup's rows
             const int start = len > 128 ? len - 128 : 0, nwin = len - start;
             if (tid() < nwin) {
