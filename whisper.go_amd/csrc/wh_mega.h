@@ -54,6 +54,7 @@ constexpr int THREADS = 512;
 constexpr int WAVES = THREADS / 64;
 constexpr int FLAG_STRIDE = 16;
 constexpr int PKV = 8;      // float4 of K (and of V) per thread: 256-key chunks
+constexpr int CMAX = 8;     // key chunks per head (2048 encoder frames)
 constexpr int PFC2 = 3;     // fc2 input passes: n_state <= 64*3*32/4 = 1536
 // register slots (rows) per wave: a workgroup holds WAVES * slots rows of each kind
 constexpr int SCQ = 8;      // cross query rows of one head: 64 = 8 * 8

@@ -179,35 +179,39 @@ __device__ __forceinline__ void publish(unsigned *flags, int slot, unsigned g) {
     if (tid() == 0) st_u(&flags[(unsigned)slot * FS], g);
 }
 
-// Wait until flags[(first + i) * FS] >= g for i < count (count <= 512).
+// Wait until flags[(first + i) * FS] >= g for i < count (1 <= count <= 256).
 // Wave 0 polls with two rounds of loads in flight (the older round is tested
-// while the newer one travels); the other waves wait at the barrier.
+// while the newer one travels); the other waves wait at the barrier. The loads
+// are unconditional (lanes past count re-read the last flag, one request per
+// wave): predicated loads let the compiler test each value inside its own
+// branch, right behind its load, which serialises the round trips. Addresses
+// are a scalar base plus 32-bit lane offsets to keep the loop's registers few.
 __device__ __forceinline__ void wait_flags(const unsigned *flags, int first, int count, unsigned g, unsigned *err) {
     const int t = tid();
     if (t < 64) {
-        unsigned v0[8], v1[8];
+        typedef __attribute__((address_space(1))) const unsigned gcu;
+        gcu *base = glob<gcu>(flags);
+        gcu *perr = glob<gcu>(err);
+        unsigned off[4], v0[4], v1[4];
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int i = t + 64 * k;
-            v0[k] = i < count ? ld_u(&flags[(unsigned)(first + i) * FS]) : 0xFFFFFFFFu;
-        }
-        unsigned spins = 0;
-        for (;;) {
+        for (int k = 0; k < 4; k++) off[k] = (unsigned)(first + min(t + 64 * k, count - 1)) * FS;
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const int i = t + 64 * k;
-                v1[k] = i < count ? ld_u(&flags[(unsigned)(first + i) * FS]) : 0xFFFFFFFFu;
-            }
-            bool ok = true;
+        for (int k = 0; k < 4; k++) v0[k] = __hip_atomic_load(base + off[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        unsigned e0 = __hip_atomic_load(perr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (unsigned spins = 0;; spins++) {
 #pragma unroll
-            for (int k = 0; k < 8; k++) ok &= v0[k] >= g;
-            if (__all(ok)) break;
-            if (++spins > SPIN_MAX || ((spins & 255) == 0 && ld_u(err))) {
+            for (int k = 0; k < 4; k++)
+                v1[k] = __hip_atomic_load(base + off[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned e1 = __hip_atomic_load(perr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned lo = min(min(v0[0], v0[1]), min(v0[2], v0[3]));
+            if (__all(lo >= g)) break;
+            if (e0 != 0 || spins > SPIN_MAX) {  // another workgroup gave up, or this wait expired
                 if (t == 0) atomicOr(err, 1u);
                 break;
             }
 #pragma unroll
-            for (int k = 0; k < 8; k++) v0[k] = v1[k];
+            for (int k = 0; k < 4; k++) v0[k] = v1[k];
+            e0 = e1;
         }
     }
     __syncthreads();
@@ -715,8 +719,13 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 }
                 wait_flags(iflags, ih * a.C, a.C, gB, a.err);
                 TRACE(step, l, 2, 1);
-                float M = -INFINITY;
-                for (int i = 0; i < a.C; i++) M = fmaxf(M, ld_f(&a.cmax[ih * a.C + i]));
+                // chunk maxima of the head: all loads in flight before the first use
+                float cm[CMAX];
+#pragma unroll
+                for (int i = 0; i < CMAX; i++) cm[i] = i < a.C ? ld_f(&a.cmax[ih * a.C + i]) : -INFINITY;
+                float M = cm[0];
+#pragma unroll
+                for (int i = 1; i < CMAX; i++) M = fmaxf(M, cm[i]);
                 float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
                 float es = 0.0f;
 #pragma unroll
@@ -767,11 +776,18 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 }
                 __syncthreads();
                 if (last_flag && tid() < 64) {
+                    float ps[CMAX], po[CMAX];
+#pragma unroll
+                    for (int i = 0; i < CMAX; i++) {
+                        const float *p2 = a.parts + (size_t)(ih * a.C + min(i, a.C - 1)) * 65;
+                        ps[i] = i < a.C ? ld_f(&p2[64]) : 0.0f;
+                        po[i] = i < a.C ? ld_f(&p2[tid()]) : 0.0f;
+                    }
                     float sum = 0.0f, o = 0.0f;
-                    for (int i = 0; i < a.C; i++) {
-                        const float *p2 = a.parts + (size_t)(ih * a.C + i) * 65;
-                        sum += ld_f(&p2[64]);
-                        o += ld_f(&p2[tid()]);
+#pragma unroll
+                    for (int i = 0; i < CMAX; i++) {
+                        sum += ps[i];
+                        o += po[i];
                     }
                     st_f(&a.attn[ih * 64 + tid()], o * (1.0f / sum));
                     __builtin_amdgcn_s_waitcnt(0);

@@ -279,7 +279,7 @@ int mega_setup(wh_seq &s) {
     // per-workgroup row capacities of the kernel's register slots
     auto per = [&](int rows, int n) { return (rows + n - 1) / n; };
     const int NW = mega::WAVES;
-    if (W < 8 || items > W || W > 512 || per(d, W) > NW * mega::SD || per(4 * d, W) > NW * mega::SE) return WH_OK;
+    if (C > mega::CMAX || W < 8 || items > W || W > 256 || H > 256 || per(d, W) > NW * mega::SD || per(4 * d, W) > NW * mega::SE) return WH_OK;
     if (mega::lds_bytes(d, L, m.n_vocab, W) + 64 > (size_t)lds_max) return WH_OK;
     auto fits32 = [](const DevMat &x) { return (uint64_t)x.rows * x.nb * 32 < (1ull << 32); };
     if (!fits32(m.tok)) return WH_OK;
