@@ -44,7 +44,7 @@ struct MegaArgs {
     float *out_logits;    // raw logits of the last step, or null
     int32_t *state_out;   // produced, prev, streak, final phase index
     // exchange buffers
-    float *xg, *sa, *x2, *hbuf, *attn, *cmax, *parts, *pval, *eot_logit;
+    float *xg, *sa, *x2, *hbuf, *attn, *cmax, *parts, *pval, *eot_logit, *qx;
     int32_t *pidx;
     unsigned *flags, *hflags, *hcount, *err;
     unsigned g0;
@@ -54,19 +54,20 @@ constexpr int THREADS = 512;
 constexpr int WAVES = THREADS / 64;
 constexpr int FLAG_STRIDE = 16;
 constexpr int PKV = 8;      // float4 of K (and of V) per thread: 256-key chunks
-constexpr int CMAX = 8;     // key chunks per head (2048 encoder frames)
+constexpr int CMIN = 4;     // key chunks per head at least (so a chunk's q rows fit SCQ)
+constexpr int CMAX = 8;     // key chunks per head at most (2048 encoder frames)
 constexpr int PFC2 = 3;     // fc2 input passes: n_state <= 64*3*32/4 = 1536
 // register slots (rows) per wave: a workgroup holds WAVES * slots rows of each kind
-constexpr int SCQ = 8;      // cross query rows of one head: 64 = 8 * 8
+constexpr int SCQ = 2;      // cross query rows of one chunk: 64 / C <= 16 (C >= 4)
 constexpr int SQ = 4;       // q,k,v side rows
 constexpr int SO = 2;       // self-attention output side rows
 constexpr int SD = 2;       // cross output rows (also fc2 rows)
 constexpr int SE = 5;       // fc1 rows
 constexpr int TS = 6;       // logits rows per chunk
 
-// Dynamic LDS bytes of the kernel for n_state d, L layers, V vocabulary rows
-// and a grid of W workgroups.
-size_t lds_bytes(int d, int L, int V, int W);
+// Dynamic LDS bytes of the kernel for n_state d, L layers, V vocabulary rows,
+// a grid of W workgroups and chunk_len keys per chunk.
+size_t lds_bytes(int d, int L, int V, int W, int chunk_len);
 
 }  // namespace mega
 }  // namespace wh

@@ -555,6 +555,24 @@ __device__ __forceinline__ void side_compute(const Side<TYPE> &S, const MegaArgs
     }
 }
 
+// Stage K rows [t0, t1) of head ih (a [enc_len][64] block of crossK) into LDS
+// kst in the same layout with direct global->LDS loads (1 KiB per wave
+// instruction), issued by waves 1.. only: wave 0 polls flags and its vector
+// memory counter must stay free of long loads.
+__device__ __forceinline__ void stage_k(const float *crossK, int enc_len, int ih, int t0, int t1, float *kst) {
+    const int wave = uni(tid() >> 6), lane = tid() & 63;
+    if (wave == 0) return;
+    const float *src = crossK + ((size_t)ih * enc_len + t0) * 64;
+    const int nvec = (t1 - t0) * 16;  // 16-byte vectors
+    const int nblk = (nvec + 63) / 64;
+    for (int b = wave - 1; b < nblk; b += NW - 1) {
+        const int v = b * 64 + lane;
+        if (v < nvec)
+            __builtin_amdgcn_global_load_lds((void __attribute__((address_space(1))) *)(src + 4 * v),
+                                             (void __attribute__((address_space(3))) *)(kst + b * 256), 16, 0, 0);
+    }
+}
+
 template <int TYPE>
 __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
     extern __shared__ __align__(16) float lds[];
@@ -573,6 +591,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
     float *qh = red + 64;                 // [64] q of this workgroup's head
     float *sc = qh + 64;                  // [32*PKV] scores of this workgroup's chunk
     int *pen = (int *)(sc + 32 * PKV);    // [pen_floats] window counts of this workgroup's vocabulary rows
+    float *kst = (float *)pen + pen_floats(a.V, gridDim.x);  // [chunk_len * 64] K rows of this item's chunk
     __shared__ unsigned last_flag;
 
     {
@@ -588,6 +607,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
     const bool has_side = q1 > q0 || o1 > o0;
     const int ih = has_item ? item / a.C : 0, ic = has_item ? item % a.C : 0;
     const int t0 = ic * a.chunk_len, t1 = min(t0 + a.chunk_len, a.enc_len);
+    // this item's share of its head's cross-query rows
+    const int cq0 = ih * 64 + ic * 64 / a.C, cq1 = ih * 64 + (ic + 1) * 64 / a.C;
     const int rd0 = (int)((long)w * d / W), rd1 = (int)((long)(w + 1) * d / W);
     const int rf0 = (int)((long)w * 4 * d / W), rf1 = (int)((long)(w + 1) * 4 * d / W);
     const int rv0 = (int)((long)w * a.V / W), rv1 = (int)((long)(w + 1) * a.V / W);
@@ -624,29 +645,21 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
             }
             TRACE(step, 0, 7, 2);
             publish(a.flags, w, ++g);
+            if (has_item) stage_k(ls[0].crossK, a.enc_len, ih, t0, t1, kst);
         }
         for (int l = 0; l < L; l++) {
             const unsigned gin = g;  // x_l complete when every workgroup flag reaches gin
-            // ---------------- B: cross q and scores (items) / side rows ----------------
+            // ---------------- B1: cross q rows (items) / side rows ----------------
             {
-                const int lane = tid() & 63, wave = tid() >> 6;
+                const int lane = tid() & 63;
                 TRACE(step, l, 1, 0);
                 const MegaLayer &Ly = ls[l];
                 if (has_item) {
-                    float4 kr[PKV];
                     Pre<TYPE, SCQ> pc;
                     LnPar p2;
-                    prefetch<TYPE, SCQ, 1>(pc, uview(Ly.cq), nbd, ih * 64, ih * 64 + 64);
-                    gf *K = glob<gf>(Ly.crossK) + (size_t)ih * a.enc_len * 64;
-                    const int tt = tid();
-#pragma unroll
-                    for (int j = 0; j < PKV; j++) {
-                        // rows past the chunk re-read its last row; the scores drop them
-                        const int t = min(t0 + (j * NT + tt) / 16, t1 - 1);
-                        kr[j] = ld16f(K + (unsigned)t * 64u + 4u * (unsigned)(tt & 15));
-                    }
+                    prefetch<TYPE, SCQ, 1>(pc, uview(Ly.cq), nbd, cq0, cq1);
                     ln_load(p2, glob<gf>(Ly.ln2w), glob<gf>(Ly.ln2b), d);
-                    const float qb = lane_bias<SCQ>(glob<gf>(Ly.cqb), ih * 64, ih * 64 + 64);
+                    const float qb = lane_bias<SCQ>(glob<gf>(Ly.cqb), cq0, cq1);
                     wait_flags(a.flags, 0, W, gin, a.err);
                     TRACE(step, l, 1, 1);
                     if (l > 0) xload_pad(xs, a.xg, d);
@@ -658,34 +671,9 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                     layernorm(x1s, xn, d, p2, red);
                     TRACE(step, l, 1, 4);
                     float out[SCQ];
-                    row_dots<TYPE, SCQ, 1>(pc, nbd, ih * 64, ih * 64 + 64, xn, out);
-                    {
-                        const int r = lane_row<SCQ>(ih * 64, ih * 64 + 64);
-                        if (r >= 0) qh[r - ih * 64] = pick<SCQ>(out, lane) + qb;
-                    }
-                    __syncthreads();
-                    TRACE(step, l, 1, 5);
-                    const float4 q4 = ((const float4 *)qh)[tid() & 15];
-                    float mx = -INFINITY;
-#pragma unroll
-                    for (int j = 0; j < PKV; j++) {
-                        const int t = t0 + (j * NT + tid()) / 16;
-                        const float part =
-                            row_sum16(q4.x * kr[j].x + q4.y * kr[j].y + q4.z * kr[j].z + q4.w * kr[j].w);
-                        if (t < t1) {
-                            const float s = part * a.scale;
-                            if ((tid() & 15) == 0) sc[t - t0] = s;
-                            mx = fmaxf(mx, s);
-                        }
-                    }
-                    mx = wave_max(mx);
-                    if (lane == 0) red[wave] = mx;
-                    __syncthreads();
-                    if (tid() == 0) {
-                        float m = red[0];
-                        for (int i = 1; i < NW; i++) m = fmaxf(m, red[i]);
-                        st_f(&a.cmax[item], m);
-                    }
+                    row_dots<TYPE, SCQ, 1>(pc, nbd, cq0, cq1, xn, out);
+                    const int r = lane_row<SCQ>(cq0, cq1);
+                    if (r >= 0) st_f(&a.qx[r], pick<SCQ>(out, lane) + qb);
                     TRACE(step, l, 1, 2);
                     publish(iflags, item, ++g);
                 } else {
@@ -701,7 +689,49 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                     ++g;
                 }
             }
+            const unsigned gB1 = g;
+            // ---------------- B2: scores of the chunk against the head's q ----------------
+            ++g;
             const unsigned gB = g;
+            if (has_item) {
+                const int lane = tid() & 63, wave = tid() >> 6;
+                TRACE(step, l, 0, 0);
+                wait_flags(iflags, ih * a.C, a.C, gB1, a.err);
+                TRACE(step, l, 0, 1);
+                if (tid() < 32) {
+                    const uint64_t v = __hip_atomic_load((const uint64_t *)(a.qx + ih * 64) + tid(), __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+                    *(float2 *)&qh[2 * tid()] =
+                        make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+                }
+                __syncthreads();
+                const float4 q4 = ((const float4 *)qh)[tid() & 15];
+                const float4 *k4 = (const float4 *)kst;
+                float mx = -INFINITY;
+#pragma unroll
+                for (int j = 0; j < PKV; j++) {
+                    const int tu = t0 + (j * NT + tid()) / 16;
+                    // keys past the chunk re-read its last staged key; the scores drop them
+                    const int t = min(tu, t1 - 1);
+                    const float4 kr = k4[(t - t0) * 16 + (tid() & 15)];
+                    const float part = row_sum16(q4.x * kr.x + q4.y * kr.y + q4.z * kr.z + q4.w * kr.w);
+                    if (tu < t1) {
+                        const float s = part * a.scale;
+                        if ((tid() & 15) == 0) sc[tu - t0] = s;
+                        mx = fmaxf(mx, s);
+                    }
+                }
+                mx = wave_max(mx);
+                if (lane == 0) red[wave] = mx;
+                __syncthreads();
+                if (tid() == 0) {
+                    float m = red[0];
+                    for (int i = 1; i < NW; i++) m = fmaxf(m, red[i]);
+                    st_f(&a.cmax[item], m);
+                }
+                TRACE(step, l, 0, 2);
+                publish(iflags, item, gB);
+            }
             // ---------------- C: softmax weights, partial P.V, head combine ----------------
             ++g;
             const unsigned gC = g;
@@ -868,6 +898,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 Pre<TYPE, SD * PFC2> pf;
                 prefetch<TYPE, SD * PFC2, PFC2>(pf, uview(Ly.fc2), nbf, rd0, rd1);
                 const float fb = lane_bias<SD>(glob<gf>(Ly.fc2b), rd0, rd1);
+                // the next layer's K chunk (this layer's was consumed in B2)
+                if (has_item && l + 1 < L) stage_k(ls[l + 1].crossK, a.enc_len, ih, t0, t1, kst);
                 wait_flags(a.flags, 0, W, gE, a.err);
                 TRACE(step, l, 5, 1);
                 xload_pad(xn, a.hbuf, 4 * d);
@@ -999,14 +1031,15 @@ extern "C" int wh_mega_trace_read(void *out, size_t bytes) {
 }
 #endif
 
-size_t lds_bytes(int d, int L, int V, int W) {
+size_t lds_bytes(int d, int L, int V, int W, int chunk_len) {
     const int d36 = ((d + 31) / 32) * 36;
-    return sizeof(float) * (size_t)(layer_floats(L) + 6 * d36 + d + 64 * 4 + 32 * PKV + pen_floats(V, W));
+    return sizeof(float) *
+           (size_t)(layer_floats(L) + 6 * d36 + d + 64 * 4 + 32 * PKV + pen_floats(V, W) + chunk_len * 64);
 }
 
 int launch_decode(uint32_t type, int grid, const MegaArgs &a, hipStream_t st) {
     void *args[] = {(void *)&a};
-    const size_t shmem = lds_bytes(a.d, a.L, a.V, grid);
+    const size_t shmem = lds_bytes(a.d, a.L, a.V, grid, a.chunk_len);
     const void *fn = nullptr;
     switch (type) {
     case 2: fn = (const void *)k_decode<2>; break;

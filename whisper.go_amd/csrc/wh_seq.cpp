@@ -273,14 +273,16 @@ int mega_setup(wh_seq &s) {
     if (hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, m.device) != hipSuccess)
         return WH_OK;
     const int W = std::min(env_int("WHISPER_HIP_GRID", dev_cus), dev_cus);
-    const int chunk = 32 * mega::PKV;
-    const int C = (s.enc_len + chunk - 1) / chunk;
+    // C >= CMIN chunks of at most 32*PKV keys; the last chunk is not empty
+    const int C = std::max(mega::CMIN, (s.enc_len + 32 * mega::PKV - 1) / (32 * mega::PKV));
+    const int chunk = (s.enc_len + C - 1) / C;
+    if (s.enc_len < 16 || (C - 1) * chunk >= s.enc_len || chunk > 32 * mega::PKV) return WH_OK;
     const int items = H * C;
     // per-workgroup row capacities of the kernel's register slots
     auto per = [&](int rows, int n) { return (rows + n - 1) / n; };
     const int NW = mega::WAVES;
     if (C > mega::CMAX || W < 8 || items > W || W > 256 || H > 256 || per(d, W) > NW * mega::SD || per(4 * d, W) > NW * mega::SE) return WH_OK;
-    if (mega::lds_bytes(d, L, m.n_vocab, W) + 64 > (size_t)lds_max) return WH_OK;
+    if (mega::lds_bytes(d, L, m.n_vocab, W, chunk) + 64 > (size_t)lds_max) return WH_OK;
     auto fits32 = [](const DevMat &x) { return (uint64_t)x.rows * x.nb * 32 < (1ull << 32); };
     if (!fits32(m.tok)) return WH_OK;
     for (const Layer &l : m.layers)
@@ -354,7 +356,7 @@ int mega_setup(wh_seq &s) {
     const int FS = mega::FLAG_STRIDE;
 #define MALLOC(p, n) do { if ((rc = s.alloc(&(p), (n)))) return rc; } while (0)
     MALLOC(a.xg, (size_t)d); MALLOC(a.sa, (size_t)2 * d); MALLOC(a.x2, (size_t)d); MALLOC(a.hbuf, (size_t)4 * d);
-    MALLOC(a.attn, (size_t)d); MALLOC(a.cmax, (size_t)items); MALLOC(a.parts, (size_t)items * 65);
+    MALLOC(a.attn, (size_t)d); MALLOC(a.qx, (size_t)d); MALLOC(a.cmax, (size_t)items); MALLOC(a.parts, (size_t)items * 65);
     MALLOC(a.pval, (size_t)2 * W); MALLOC(a.pidx, (size_t)2 * W); MALLOC(a.eot_logit, 1);
     // workgroup flags [W] then item flags [items]
     MALLOC(a.flags, (size_t)(W + items) * FS); MALLOC(a.hflags, (size_t)H * FS);
