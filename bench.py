@@ -76,6 +76,22 @@ def generate_n(seq, n):
     return out
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_persistent_large-v3_q8_0.md")
+
+
+def measured_traffic(config, qtype, persistent):
+    """HBM bytes per token of the persistent kernel on large-v3 Q8_0, from the
+    committed rocprofv3 --pmc summary (FETCH_SIZE x 2 + WRITE_SIZE x 1, scaled
+    by a device-to-device copy of known size), or None for other workloads."""
+    if not (persistent and config == "large-v3" and qtype == "Q8_0") or not os.path.exists(TRAFFIC_PROFILE):
+        return None
+    with open(TRAFFIC_PROFILE) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_token:"):
+                return int(line.split(":")[1])
+    return None
+
+
 def copy_calibration(wh, mib):
     """Device-to-device copies of a known size: their FETCH_SIZE / WRITE_SIZE in
     a rocprofv3 --pmc run give the scale factor for the decode kernel's counters."""
@@ -134,6 +150,8 @@ def run_decode(args):
     dms, dcount, dbytes = prof[dom]
     achieved = dbytes / (dms * 1e-3) / 1e9 if dms > 0 else 0.0
     value = args.steps / dt
+    tpt = measured_traffic(args.config, args.qtype, persistent)
+    traffic = round(tpt * args.steps / max(dcount, 1)) if tpt and dom == "decode_persistent" else None
     out = {
         "metric": "decode tokens/s (large-v3 Q8_0, bs=1)" if args.config == "large-v3" and args.qtype == "Q8_0"
         else f"decode tokens/s ({args.config} {args.qtype}, bs=1)",
@@ -150,7 +168,9 @@ def run_decode(args):
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "launches": dcount, "avg_launch_us": round(dms * 1e3 / max(dcount, 1), 3),
-                     "bytes_per_launch": round(dbytes / max(dcount, 1)), "traffic": None},
+                     "bytes_per_launch": round(dbytes / max(dcount, 1)), "traffic": traffic,
+                     "traffic_source": "rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE of this launch shape, "
+                                       "profiles/decode_persistent_large-v3_q8_0.md" if traffic else None},
         "kernel_ms_per_step": {k: round(v / args.steps, 4) for k, v in kern_ms.items()},
         "stopped_at_step": next((i + 1 for i, t in enumerate(tokens) if t == dec.eot), None),
     }
@@ -228,7 +248,8 @@ def main():
     ap.add_argument("--qtype", default="Q8_0", choices=sorted(QNAMES))
     ap.add_argument("--multikernel-steps", type=int, default=32,
                     help="also time this many steps with one launch per kernel (0 = skip)")
-    ap.add_argument("--cpu-tokens", type=int, default=3, help="oracle steps timed for cpu_baseline (0 = skip)")
+    ap.add_argument("--cpu-tokens", type=int, default=30,
+                    help="oracle steps timed for cpu_baseline, about 0.4 s each (0 = skip)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="first copy this many MiB device to device (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--gemv", action="store_true", help="run the standalone GEMV microbench instead")
@@ -236,7 +257,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(streams shard data-parallel across GPUs with no collective; see DESIGN.md)", file=sys.stderr)
+              "(streams shard data-parallel across GPUs with no collective)", file=sys.stderr)
         sys.exit(2)
     if args.gemv:
         run_gemv(args)
