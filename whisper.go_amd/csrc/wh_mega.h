@@ -43,26 +43,42 @@ struct MegaArgs {
     int32_t *out_tokens;  // [n_steps]
     float *out_logits;    // raw logits of the last step, or null
     int32_t *state_out;   // produced, prev, streak, final phase index
-    // exchange buffers
-    float *xg, *sa, *x2, *hbuf, *attn, *cmax, *parts, *pval, *eot_logit, *qx;
-    int32_t *pidx;
-    unsigned *flags, *hflags, *hcount, *err;
+    // Exchange buffers of 8-byte {float value (low word), phase (high word)}
+    // pairs, each stored with one atomic 64-bit store: a reader polls the
+    // pairs themselves until they carry the phase it waits for.
+    uint64_t *xg;         // [d] x_l
+    uint64_t *sa;         // [2][d] sa_l by layer parity
+    uint64_t *x2;         // [d]
+    uint64_t *hbuf;       // [4d] GELU(fc1)
+    uint64_t *attn;       // [d] cross-attention output
+    uint64_t *qx;         // [d] cross query
+    uint64_t *cmax;       // [H*C] chunk score maxima
+    uint64_t *parts;      // [H*C][65] chunk P.V sums and weight sums
+    uint64_t *part;       // [W][4] argmax partials: value, index, value without EOT, index
+    uint64_t *eot_logit;  // [1]
+    unsigned *err;
     unsigned g0;
 };
 
 constexpr int THREADS = 512;
 constexpr int WAVES = THREADS / 64;
-constexpr int FLAG_STRIDE = 16;
-constexpr int PKV = 8;      // float4 of K (and of V) per thread: 256-key chunks
-constexpr int CMIN = 4;     // key chunks per head at least (so a chunk's q rows fit SCQ)
-constexpr int CMAX = 8;     // key chunks per head at most (2048 encoder frames)
+constexpr int CWAVES = WAVES - 1;  // waves 1.. hold weight rows; wave 0 polls, exchanges and publishes
+constexpr int PKV = 9;      // scores: 32 keys per pass of 512 threads, 288 keys per chunk at most
+constexpr int PVK = 10;     // P.V: float4 of V per compute thread, 448 * 10 / 16 = 280 keys at most
+constexpr int CHUNK_MAX = 280;
+constexpr int CMIN = 4;     // key chunks per head at least (a chunk's cross-query rows fit SCQ slots)
+constexpr int CMAX = 8;     // key chunks per head at most (2240 encoder frames)
 constexpr int PFC2 = 3;     // fc2 input passes: n_state <= 64*3*32/4 = 1536
-// register slots (rows) per wave: a workgroup holds WAVES * slots rows of each kind
-constexpr int SCQ = 2;      // cross query rows of one chunk: 64 / C <= 16 (C >= 4)
-constexpr int SQ = 4;       // q,k,v side rows
+constexpr int XD = 21;      // exchange pairs per lane of a d-vector load: n_state <= 1344
+constexpr int XH = 12;      // exchange pairs per compute lane of the 4d-vector load: 4d <= 7*64*12
+constexpr int XP = 9;       // exchange pairs per lane of a head's chunk sums: CMAX * 65 <= 576
+constexpr int XT = 16;      // exchange pairs per lane of the argmax partials: 4 * 256
+// register slots (rows) per compute wave: a workgroup holds CWAVES * slots rows of each kind
+constexpr int SCQ = 3;      // cross query rows of one chunk: 64 / C <= 21 (C >= 4)
+constexpr int SQ = 5;       // q,k,v side rows (also the slots the cross query rows use)
 constexpr int SO = 2;       // self-attention output side rows
-constexpr int SD = 2;       // cross output rows (also fc2 rows)
-constexpr int SE = 5;       // fc1 rows
+constexpr int SD = 1;       // cross output rows (also fc2 rows)
+constexpr int SE = 3;       // fc1 rows
 constexpr int TS = 6;       // logits rows per chunk
 
 // Dynamic LDS bytes of the kernel for n_state d, L layers, V vocabulary rows,

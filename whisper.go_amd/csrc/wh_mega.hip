@@ -9,31 +9,39 @@
 // Both are computed off the critical path by "side" workgroups while the
 // cross-attention runs. One workgroup of 512 threads per CU walks these
 // phases; each boundary is a data dependency between workgroups:
-//   S  (once per step) embedding; side workgroups: sa_0 rows
-//   B  item workgroups (one per (head, key chunk)): x1 = x_l + sa_l, LN2, q of
-//      the head (64 rows of the cross query matrix), scores of the chunk and
-//      its maximum. Side workgroups: LN1(x_l), q,k,v rows -> KV cache, and the
-//      rows of sa_{l+1}.
-//   C  item workgroups: head maximum, fast-exp weights, partial sum and P.V;
-//      the last chunk of a head to finish combines the head
-//   D  cross output rows: x2 = x1 + (Wo_c . attn + ob_c)
-//   E  LN3 + fc1 rows + GELU
-//   F  fc2 rows: x_{l+1} = x2 + (W2 . h + b2)
-//   T  final LN + tied logits rows + repetition penalty + partial argmax;
-//      every workgroup reduces the partials and takes the same next token.
-// Each phase first issues the loads of everything it can (weight rows, LN
-// parameters, biases, constant vectors) and then waits for its inputs.
+//   S   (once per step) embedding; side workgroups: sa_0 rows
+//   B1  item workgroups (one per (head, key chunk)): x1 = x_l + sa_l, LN2 and
+//       the chunk's share of the head's cross-query rows. Side workgroups:
+//       LN1(x_l), q,k,v rows -> KV cache, and the rows of sa_{l+1}.
+//   B2  items: the head's q (head-local exchange), scores of the chunk
+//       against its K rows (staged in LDS a layer ahead), chunk maximum
+//   C   items: head maximum, fast-exp weights, partial sum and P.V; the last
+//       chunk of a head to finish combines the head
+//   D   cross output rows: x2 = x1 + (Wo_c . attn + ob_c)
+//   E   LN3 + fc1 rows + GELU
+//   F   fc2 rows: x_{l+1} = x2 + (W2 . h + b2)
+//   T   final LN + tied logits rows + repetition penalty + partial argmax;
+//       every workgroup reduces the partials and takes the same next token.
 //
-// Cross-workgroup data moves through relaxed agent-scope atomic loads/stores
-// (they bypass the non-coherent caches) and phase flags written after
-// `s_waitcnt` has retired the data stores. Every wait is bounded: on timeout
-// the error word is set, later waits return at once, the token loop stops and
-// the host reports a failure.
+// Roles of the 8 waves of a workgroup. The vector memory counter of a wave
+// retires in order, so a wave that waits for one load waits for every older
+// one. Waves 1..7 (compute waves) hold all weight rows: right after the dot
+// products of a phase they issue the loads of the next phase's rows, which
+// then stream while the flags travel. Wave 0 (communication wave) never has a
+// weight load in flight: it polls the flags, loads the exchanged vectors into
+// LDS, stores the results the compute waves post in an LDS outbox, retires
+// those stores with s_waitcnt and publishes the phase flag. LDS-only work
+// (scores) is shared by all waves.
+//
+// Cross-workgroup data moves through relaxed agent-scope atomic loads and
+// stores, which bypass the non-coherent caches. Every wait is bounded: on timeout the
+// error word is set, later waits return at once, the token loop stops and the
+// host reports a failure.
 //
 // Addressing: the layer descriptors are copied into LDS once per launch; each
 // phase reads the pointers it needs from there into scalar registers
 // (readfirstlane) as global-address-space pointers, so weight loads are
-// `global_load ... v_offset, s[base]` issued up front.
+// `global_load ... v_offset, s[base]`.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -50,8 +58,9 @@ namespace mega {
 
 constexpr int NT = THREADS;
 constexpr int NW = WAVES;
-constexpr int NC = NW;  // waves holding weight rows (all: more loads in flight beat a load-free poller)
-constexpr int FS = FLAG_STRIDE;
+constexpr int NC = CWAVES;    // compute waves 1..NC
+constexpr int NCT = NC * 64;  // compute threads
+constexpr int OUTBOX = 64;    // posted (row, value) pairs per phase
 constexpr unsigned SPIN_MAX = 1u << 22;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -99,8 +108,11 @@ __device__ __forceinline__ int tid() {
 // A value that is the same on every lane, kept in a scalar register.
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-// Index of this wave among the NC waves holding weight rows (-1: none).
-__device__ __forceinline__ int cwave() { return uni(tid() >> 6) - (NW - NC); }
+// Compute-wave index 0..NC-1 of this wave, or -1 for the communication wave.
+__device__ __forceinline__ int cwave() { return uni(tid() >> 6) - 1; }
+__device__ __forceinline__ bool comm() { return uni(tid() >> 6) == 0; }
+// Compute-thread index 0..NCT-1 (0 in the communication wave).
+__device__ __forceinline__ int ctid() { return max(tid() - 64, 0); }
 
 // A pointer that is the same on every lane, moved to scalar registers and
 // typed as global memory.
@@ -158,89 +170,179 @@ __device__ __forceinline__ float wave_max(float v) {
 // Diagnostic build only: thread 0 of every workgroup stamps the constant
 // 100 MHz clock at each phase's start (point 0), after its wait (1) and before
 // its publish (2), for the first TR_STEPS steps of a launch; points 3.. split
-// a phase's work. Phase 6 is T, 7 the step-start phase S.
+// a phase's work. Phase 0 is B2, 6 is T, 7 the step-start phase S.
 constexpr int TR_STEPS = 2, TR_MAXL = 33, TR_PTS = 8, TR_MAXW = 256;
+#ifdef WH_MEGA_TRACE_CYCLES
+#define WH_STAMP() clock64()
+#else
+#define WH_STAMP() wall_clock64()
+#endif
 __device__ long long g_trace[TR_STEPS * TR_MAXL * 8 * TR_PTS * TR_MAXW];
 #define TRACE(step, l, ph, pt)                                                                                        \
     do {                                                                                                              \
         if ((step) < TR_STEPS && (l) < TR_MAXL && blockIdx.x < TR_MAXW && tid() == 0)                                 \
-            g_trace[((((step) * TR_MAXL + (l)) * 8 + (ph)) * TR_PTS + (pt)) * TR_MAXW + blockIdx.x] = wall_clock64(); \
+            g_trace[((((step) * TR_MAXL + (l)) * 8 + (ph)) * TR_PTS + (pt)) * TR_MAXW + blockIdx.x] = WH_STAMP(); \
+    } while (0)
+// the same stamp from the first compute wave
+#define TRACEC(step, l, ph, pt)                                                                                       \
+    do {                                                                                                              \
+        if ((step) < TR_STEPS && (l) < TR_MAXL && blockIdx.x < TR_MAXW && tid() == 64)                                \
+            g_trace[((((step) * TR_MAXL + (l)) * 8 + (ph)) * TR_PTS + (pt)) * TR_MAXW + blockIdx.x] = WH_STAMP(); \
     } while (0)
 #else
 #define TRACE(step, l, ph, pt) \
     do {                       \
     } while (0)
+#define TRACEC(step, l, ph, pt) \
+    do {                        \
+    } while (0)
 #endif
 
-// Retire this workgroup's coherent stores, then publish phase g in flags[slot].
-__device__ __forceinline__ void publish(unsigned *flags, int slot, unsigned g) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid() == 0) st_u(&flags[(unsigned)slot * FS], g);
-}
-
-// Wait until flags[(first + i) * FS] >= g for i < count (1 <= count <= 256).
-// Wave 0 polls with two rounds of loads in flight (the older round is tested
-// while the newer one travels); the other waves wait at the barrier. The loads
-// are unconditional (lanes past count re-read the last flag, one request per
-// wave): predicated loads let the compiler test each value inside its own
-// branch, right behind its load, which serialises the round trips. Addresses
-// are a scalar base plus 32-bit lane offsets to keep the loop's registers few.
-__device__ __forceinline__ void wait_flags(const unsigned *flags, int first, int count, unsigned g, unsigned *err) {
-    const int t = tid();
-    if (t < 64) {
-        typedef __attribute__((address_space(1))) const unsigned gcu;
-        gcu *base = glob<gcu>(flags);
-        gcu *perr = glob<gcu>(err);
-        unsigned off[4], v0[4], v1[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) off[k] = (unsigned)(first + min(t + 64 * k, count - 1)) * FS;
-#pragma unroll
-        for (int k = 0; k < 4; k++) v0[k] = __hip_atomic_load(base + off[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        unsigned e0 = __hip_atomic_load(perr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        for (unsigned spins = 0;; spins++) {
-#pragma unroll
-            for (int k = 0; k < 4; k++)
-                v1[k] = __hip_atomic_load(base + off[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const unsigned e1 = __hip_atomic_load(perr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const unsigned lo = min(min(v0[0], v0[1]), min(v0[2], v0[3]));
-            if (__all(lo >= g)) break;
-            if (e0 != 0 || spins > SPIN_MAX) {  // another workgroup gave up, or this wait expired
-                if (t == 0) atomicOr(err, 1u);
-                break;
-            }
-#pragma unroll
-            for (int k = 0; k < 4; k++) v0[k] = v1[k];
-            e0 = e1;
-        }
-    }
-    __syncthreads();
+// ---- exchange: {value, phase} pairs ------------------------------------------------
+__device__ __forceinline__ void st_pair(uint64_t *p, float v, unsigned g) {
+    __hip_atomic_store(p, ((uint64_t)g << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // LDS vectors keep each 32-element block in 36 slots: a lane reading its whole
 // block then hits 4 banks no other lane of its 16-lane group uses.
 __device__ __forceinline__ int pad(int i) { return i + ((i >> 5) << 2); }
 
-// n floats (n even, src 8-byte aligned) of a coherent exchange vector into a
-// padded LDS vector, two per 64-bit load.
-__device__ __forceinline__ void xload_pad(float *dst, const float *src, int n) {
-    for (int i = tid(); i < n / 2; i += NT) {
-        const uint64_t v = __hip_atomic_load((const uint64_t *)src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *(float2 *)&dst[pad(2 * i)] = make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+// One wave: wait until the pairs src[first + 64k + lane] (k < K, below n;
+// 1 <= n) carry phase >= g; their values are left in v. Every pair is loaded
+// up front; later rounds re-read only the pending ones. Lanes past n re-read
+// the last pair and do not wait for it. On timeout, or when another workgroup
+// gave up, the error word is set and the (stale) values are returned anyway;
+// the token loop then stops.
+template <int K>
+__device__ __forceinline__ void ll_poll(uint64_t (&v)[K], const uint64_t *src, int n, unsigned g, unsigned *err,
+                                        int first = 0) {
+    typedef __attribute__((address_space(1))) const uint64_t gcu64;
+    typedef __attribute__((address_space(1))) const unsigned gcu;
+    const int lane = first + (tid() & 63);
+    gcu64 *s8 = glob<gcu64>(src);
+    gcu *perr = glob<gcu>(err);
+#pragma unroll
+    for (int k = 0; k < K; k++)
+        v[k] = __hip_atomic_load(s8 + min(lane + 64 * k, n - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned e = __hip_atomic_load(perr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (unsigned spins = 0;; spins++) {
+        bool ok = true;
+#pragma unroll
+        for (int k = 0; k < K; k++) ok &= (lane + 64 * k >= n) || (unsigned)(v[k] >> 32) >= g;
+        if (__all(ok)) break;
+        if (e != 0 || spins > SPIN_MAX) {  // another workgroup gave up, or this wait expired
+            if ((tid() & 63) == 0) atomicOr(err, 1u);
+            break;
+        }
+#pragma unroll
+        for (int k = 0; k < K; k++)
+            if ((unsigned)(v[k] >> 32) < g)
+                v[k] = __hip_atomic_load(s8 + min(lane + 64 * k, n - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        e = __hip_atomic_load(perr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
-// same into a plain LDS vector
-__device__ __forceinline__ void xload(float *dst, const float *src, int n) {
-    for (int i = tid(); i < n / 2; i += NT) {
-        const uint64_t v = __hip_atomic_load((const uint64_t *)src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *(float2 *)&dst[2 * i] = make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+
+// ll_poll, then the values into LDS dst at the same indices (padded when PAD).
+template <int K, bool PAD>
+__device__ __forceinline__ void ll_load(float *dst, const uint64_t *src, int n, unsigned g, unsigned *err,
+                                        int first = 0) {
+    uint64_t v[K];
+    ll_poll<K>(v, src, n, g, err, first);
+    const int lane = first + (tid() & 63);
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int i = lane + 64 * k;
+        if (i < n) dst[PAD ? pad(i) : i] = __uint_as_float((uint32_t)v[k]);
+    }
+}
+
+// LayerNorm parameters of one wave's elements lane + 64k (k < K).
+template <int K>
+struct LnW {
+    float w[K], b[K];
+};
+template <int K>
+__device__ __forceinline__ void ln_params(LnW<K> &p, gf *w, gf *b, int n) {
+    const int lane = tid() & 63;
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int i = min(lane + 64 * k, n - 1);
+        p.w[k] = w[i];
+        p.b[k] = b[i];
+    }
+}
+
+// LayerNorm (internal/ml/ops.go:153-202) by one wave of the n values
+// x[k] = element lane + 64k, into padded LDS xo: the mean, then the mean of
+// squared deviations, sqrt in float64, each element w * (x - mean) / sd + b.
+// No barrier: the sums are wave reductions.
+template <int K>
+__device__ __forceinline__ void ln_wave(const float (&x)[K], int n, const LnW<K> &p, float *xo) {
+    const int lane = tid() & 63;
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < K; k++) s += (lane + 64 * k < n) ? x[k] : 0.0f;
+    const float mean = wave_sum(s) / (float)n;
+    float q = 0.0f;
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const float u = x[k] - mean;
+        q += (lane + 64 * k < n) ? u * u : 0.0f;
+    }
+    const float var = wave_sum(q) / (float)n;
+    const float sd = (float)sqrt((double)(var + 1e-5f));
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int i = lane + 64 * k;
+        if (i < n) xo[pad(i)] = p.w[k] * (x[k] - mean) / sd + p.b[k];
+    }
+}
+
+// Communication wave: wait for the exchanged vector src (n pairs of phase g),
+// add the plain LDS vector add when ADD (the residual x + sa), LayerNorm it
+// into padded LDS xo.
+template <int K, bool ADD>
+__device__ __forceinline__ void ll_load_ln(float *xo, const uint64_t *src, int n, unsigned g, unsigned *err,
+                                           const LnW<K> &p, const float *add) {
+    uint64_t v[K];
+    ll_poll<K>(v, src, n, g, err);
+    const int lane = tid() & 63;
+    float x[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        x[k] = __uint_as_float((uint32_t)v[k]);
+        if (ADD) x[k] += add[min(lane + 64 * k, n - 1)];
+    }
+    ln_wave<K>(x, n, p, xo);
+}
+
+// ---- outbox: compute lanes post (row, value); the communication wave stores ----
+// Lane k < K of compute wave c posts into slot c*K + k; r < 0 posts nothing.
+template <int K>
+__device__ __forceinline__ void post(int *obi, float *obv, int r, float v) {
+    static_assert(NC * K <= OUTBOX, "outbox too small");
+    const int lane = tid() & 63, cw = cwave();
+    if (cw >= 0 && lane < K) {
+        obi[cw * K + lane] = r;
+        obv[cw * K + lane] = v;
+    }
+}
+// Communication wave only, after a barrier that follows the posts: store the
+// posted values as pairs of phase g into dst. Nothing waits for the stores:
+// readers poll the pairs.
+template <int K>
+__device__ __forceinline__ void flush(const int *obi, const float *obv, uint64_t *dst, unsigned g) {
+    const int t = tid() & 63;
+    if (t < NC * K) {
+        const int r = obi[t];
+        if (r >= 0) st_pair(&dst[r], obv[t], g);
     }
 }
 
 // ---- weight rows prefetched into registers ----------------------------------------
-// Rows [r0, r1) of a workgroup; wave v takes rows r0+v, r0+v+NW, ...; lane l
-// takes blocks l, l+64, ... of each row (PASSES passes). Slot s holds row
-// k = s / PASSES of this wave and pass p = s % PASSES.
+// Rows [r0, r1) of a workgroup; compute wave c takes rows r0+c, r0+c+NC, ...;
+// lane l takes blocks l, l+64, ... of each row (PASSES passes). Slot s holds
+// row k = s / PASSES of this wave and pass p = s % PASSES.
 template <int TYPE, int MAXS>
 struct Pre {
     uint4 a[MAXS];
@@ -264,28 +366,26 @@ __device__ __forceinline__ void load_blk(const UView &m, unsigned blk, uint4 &a,
     }
 }
 
-// Loads are unconditional: a slot past the range re-reads the last valid row
-// or block (row 0 for an empty range; a cache hit) and the dot products drop
-// it, so no slot is ever undefined (undefined slots become loop-carried live
-// ranges and spill) and no branch surrounds the loads.
-template <int TYPE, int MAXS, int PASSES>
+// Slots [0, NS) load; slots [NS, MAXS) and every slot of the communication
+// wave hold zeros. Loads are unconditional: a slot past the range re-reads the
+// last valid row or block (row 0 for an empty range; a cache hit) and the dot
+// products drop it, so no slot is ever undefined (undefined slots become
+// loop-carried live ranges and spill) and no branch surrounds the loads.
+template <int TYPE, int MAXS, int PASSES, int NS = MAXS>
 __device__ __forceinline__ void prefetch(Pre<TYPE, MAXS> &P, const UView &m, int nb, int r0, int r1) {
     const int lane = tid() & 63, cw = cwave();
-    if (cw < 0) {
 #pragma unroll
-        for (int s = 0; s < MAXS; s++) {
+    for (int s = 0; s < MAXS; s++) {
+        if (s >= NS || cw < 0) {
             P.a[s] = make_uint4(0u, 0u, 0u, 0u);
             P.b[s] = make_uint4(0u, 0u, 0u, 0u);
             P.s[s] = 0u;
             P.h[s] = 0u;
+        } else {
+            const int r = max(min(r0 + cw + NC * (s / PASSES), r1 - 1), 0);
+            const int b = min(lane + 64 * (s % PASSES), nb - 1);
+            load_blk<TYPE>(m, (unsigned)r * (unsigned)nb + (unsigned)b, P.a[s], P.b[s], P.s[s], P.h[s]);
         }
-        return;
-    }
-#pragma unroll
-    for (int s = 0; s < MAXS; s++) {
-        const int r = max(min(r0 + cw + NC * (s / PASSES), r1 - 1), 0);
-        const int b = min(lane + 64 * (s % PASSES), nb - 1);
-        load_blk<TYPE>(m, (unsigned)r * (unsigned)nb + (unsigned)b, P.a[s], P.b[s], P.s[s], P.h[s]);
     }
 }
 
@@ -342,10 +442,21 @@ __device__ __forceinline__ void lds_block(const float *xs, int b, float (&xr)[32
     }
 }
 
+// A prefetched slot made opaque right before its use: otherwise the compiler
+// moves the first operations on it (the f16 scale conversion, byte extracts)
+// up into the prefetch, right behind the loads, and has to wait for each load
+// there, which makes the prefetch synchronous.
+template <int TYPE>
+__device__ __forceinline__ void opaque_slot(uint4 &a, uint4 &b, uint32_t &s, uint32_t &h) {
+    __asm__ volatile("" : "+v"(a.x), "+v"(a.y), "+v"(a.z), "+v"(a.w), "+v"(s));
+    if constexpr (TYPE == 8) __asm__ volatile("" : "+v"(b.x), "+v"(b.y), "+v"(b.z), "+v"(b.w));
+    if constexpr (TYPE == 6 || TYPE == 7) __asm__ volatile("" : "+v"(h));
+}
+
 // Row dots of the prefetched slots: out[k] (same on every lane) is the dot of
 // row r0 + cw + NC*k (cw = cwave()) with the padded LDS vector xs of nb
 // blocks. Lanes past the last block and rows past r1 compute on duplicate
-// data and add zero; the poller wave returns zeros.
+// data and add zero; the communication wave returns zeros.
 template <int TYPE, int MAXS, int PASSES>
 __device__ __forceinline__ void row_dots(const Pre<TYPE, MAXS> &P, int nb, int r0, int r1, const float *xs,
                                          float (&out)[MAXS / PASSES]) {
@@ -363,9 +474,11 @@ __device__ __forceinline__ void row_dots(const Pre<TYPE, MAXS> &P, int nb, int r
         for (int k = 0; k < K; k++) {
             const int s = k * PASSES + p;
             const int r = r0 + cw + NC * k;
-            const float v = block_dot<TYPE>(P.a[s], P.b[s], P.s[s], P.h[s], xr);
+            uint4 qa = P.a[s], qb = P.b[s];
+            uint32_t qs = P.s[s], qh = P.h[s];
+            opaque_slot<TYPE>(qa, qb, qs, qh);
+            const float v = block_dot<TYPE>(qa, qb, qs, qh, xr);
             out[k] += (r < r1 && b < nb) ? v : 0.0f;
-            __builtin_amdgcn_sched_barrier(0);  // decode one block at a time: bounded register use
         }
     }
 #pragma unroll
@@ -376,7 +489,7 @@ __device__ __forceinline__ void row_dots(const Pre<TYPE, MAXS> &P, int nb, int r
 // wave-uniform, so each value is written into its lane with v_writelane; a
 // select chain on the lane index is turned into a private (scratch) array.
 template <int K>
-__device__ __forceinline__ float pick(const float (&out)[K], int) {
+__device__ __forceinline__ float pick(const float (&out)[K]) {
     float v = 0.0f;
 #pragma unroll
     for (int k = 0; k < K; k++) {
@@ -387,7 +500,7 @@ __device__ __forceinline__ float pick(const float (&out)[K], int) {
 }
 
 // Per-lane bias of row r0 + cw + NC*lane (lane < K), clamped into [r0, r1);
-// the poller wave loads nothing.
+// the communication wave loads nothing.
 template <int K>
 __device__ __forceinline__ float lane_bias(gf *bias, int r0, int r1) {
     const int lane = tid() & 63, cw = cwave();
@@ -403,61 +516,15 @@ __device__ __forceinline__ int lane_row(int r0, int r1) {
     return (cw >= 0 && lane < K && r < r1) ? r : -1;
 }
 
-// LayerNorm parameters of this thread's elements t, t+NT, t+2NT (n <= 3*NT).
-struct LnPar {
-    float w[3], b[3];
-};
-__device__ __forceinline__ void ln_load(LnPar &p, gf *w, gf *b, int n) {
-    const int t = tid();
-#pragma unroll
-    for (int j = 0; j < 3; j++) {
-        const int i = min(t + NT * j, n - 1);
-        p.w[j] = w[i];
-        p.b[j] = b[i];
-    }
-}
-
-// LayerNorm (internal/ml/ops.go:153-202) of padded LDS xs[0..n) into padded
-// LDS xo: mean, then the mean of squared deviations, sqrt in float64.
-__device__ __forceinline__ void layernorm(const float *xs, float *xo, int n, const LnPar &p, float *red) {
-    const int t = tid(), lane = t & 63, wave = t >> 6;
-    float x[3];
-    float s = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 3; j++) {
-        const int i = t + NT * j;
-        x[j] = i < n ? xs[pad(i)] : 0.0f;
-        s += x[j];
-    }
-    s = wave_sum(s);
-    if (lane == 0) red[wave] = s;
-    __syncthreads();
-    float tot = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NW; i++) tot += red[i];
-    const float mean = tot / (float)n;
-    float v = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 3; j++) {
-        if (t + NT * j < n) {
-            const float u = x[j] - mean;
-            v += u * u;
-        }
-    }
-    v = wave_sum(v);
-    if (lane == 0) red[NW + wave] = v;
-    __syncthreads();
-    float tv = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NW; i++) tv += red[NW + i];
-    const float var = tv / (float)n;
-    const float sd = (float)sqrt((double)(var + 1e-5f));
-#pragma unroll
-    for (int j = 0; j < 3; j++) {
-        const int i = t + NT * j;
-        if (i < n) xo[pad(i)] = p.w[j] * (x[j] - mean) / sd + p.b[j];
-    }
-    __syncthreads();
+// The tanh-form GELU of internal/ml/ops.go:102-122 with tanh in float32 (the
+// reference takes tanh in float64; the two differ by about one float32 ulp of
+// 1 + tanh, far inside the logits tolerance). The float64 tanh is a long
+// dependent chain on the critical path of every layer.
+__device__ __forceinline__ float gelu_f32(float x) {
+#pragma clang fp contract(off)
+    const float k = 0.7978845608028654f;
+    const float inner = k * (x + 0.044715f * x * x * x);
+    return x * 0.5f * (1.0f + tanhf(inner));
 }
 
 __device__ __forceinline__ void better(float v, int i, float &bv, int &bi) {
@@ -465,11 +532,12 @@ __device__ __forceinline__ void better(float v, int i, float &bv, int &bi) {
 }
 
 // Logits rows of one chunk (<= NC*TS rows) with penalty and running argmax.
-// pen[r - rv0] is the window count of row r.
+// pen[r - rv0] is the window count of row r. The raw logit of the EOT row is
+// posted to LDS (*eotv) for the communication wave to publish.
 template <int TYPE>
 __device__ __forceinline__ void logits_chunk(const MegaArgs &a, const Pre<TYPE, TS> &P, int nb, int base, int end,
                                              const float *xn, const int *pen, int rv0, float &bv, int &bi,
-                                             float &bv2, int &bi2) {
+                                             float &bv2, int &bi2, float *eotv) {
     const int lane = tid() & 63, cw = cwave();
     float out[TS];
     row_dots<TYPE, TS, 1>(P, nb, base, end, xn, out);
@@ -485,7 +553,7 @@ __device__ __forceinline__ void logits_chunk(const MegaArgs &a, const Pre<TYPE, 
             const float s = v * a.inv_temp;
             better(s, r, bv, bi);
             if (r != a.eot) better(s, r, bv2, bi2);
-            if (r == a.eot && lane == 0) st_f(a.eot_logit, v);
+            if (r == a.eot && lane == 0) *eotv = v;
         }
     }
 }
@@ -494,78 +562,78 @@ __device__ __forceinline__ void logits_chunk(const MegaArgs &a, const Pre<TYPE, 
 __host__ __device__ inline int layer_floats(int L) { return (int)((L * sizeof(MegaLayer) + 15) / 16 * 4); }
 __host__ __device__ inline int pen_floats(int V, int W) { return ((V + W - 1) / W + 3) / 4 * 4; }
 
-// Side work of layer l (decoder.go:780-790 under the reference mask): LN1 of
-// x_l (padded LDS xs) -> q,k,v rows [q0,q1), k and v stored in the KV cache at
-// pos; rows [o0,o1) of sa_{l+1} = Wo_{l+1} . V0_{l+1} + ob_{l+1} (V0 in v0)
-// into the exchange buffer. side_prefetch issues the loads.
+// Rows of phase B1 of one layer, loaded by the compute waves a phase ahead.
+// Item workgroups: their share of the head's cross-query rows in pq's first
+// SCQ slots and the query bias. Side workgroups (decoder.go:780-790 under the
+// reference mask): q,k,v rows and the v bias, and the next layer's
+// self-attention output rows with their bias and that layer's V0 (3 elements
+// per compute thread). The communication wave loads the LN parameters.
 template <int TYPE>
-struct Side {
+struct B1Pre {
     Pre<TYPE, SQ> pq;
     Pre<TYPE, SO> po;
-    LnPar p1;
-    float qb, ob;  // per-lane biases of the epilogue rows
+    float qb, ob;
+    float v0r[3];
 };
 
 template <int TYPE>
-__device__ __forceinline__ void side_prefetch(Side<TYPE> &S, const MegaArgs &a, const MegaLayer *ls, int l, int q0,
-                                              int q1, int o0, int o1, int nbd, float *v0) {
-    const MegaLayer &Ly = ls[l];
-    prefetch<TYPE, SQ, 1>(S.pq, uview(Ly.sqkv), nbd, q0, q1);
-    ln_load(S.p1, glob<gf>(Ly.ln1w), glob<gf>(Ly.ln1b), a.d);
-    // v rows take the v bias; k rows have none; q rows are not used
-    const int lane = tid() & 63, cw = max(cwave(), 0);
-    const int r = max(min(q0 + cw + NC * min(lane, SQ - 1), q1 - 1), 0);
-    S.qb = glob<gf>(Ly.svb)[max(r - 2 * a.d, 0)];
-    // the last layer has no next layer: its own rows are loaded and not used
-    const MegaLayer &Ln = ls[min(l + 1, a.L - 1)];
-    prefetch<TYPE, SO, 1>(S.po, uview(Ln.so), nbd, o0, o1);
-    S.ob = lane_bias<SO>(glob<gf>(Ln.sob), o0, o1);
-    gf *kv = glob<gf>(Ln.kv) + (size_t)a.H * a.ctx * 64;  // V plane, row 0 of each head
-    for (int i = tid(); i < a.d; i += NT) v0[pad(i)] = kv[(size_t)(i / 64) * a.ctx * 64 + (i % 64)];
+__device__ __forceinline__ void v0_load(float (&v0r)[3], const MegaArgs &a, const MegaLayer &Ly) {
+    gf *kv = glob<gf>(Ly.kv) + (size_t)a.H * a.ctx * 64;  // V plane, row 0 of each head
+    const int c = ctid();
+    const bool cw = cwave() >= 0;
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        const int i = min(c + NCT * j, a.d - 1);
+        v0r[j] = cw ? kv[(size_t)(i / 64) * a.ctx * 64 + (i % 64)] : 0.0f;
+    }
+}
+__device__ __forceinline__ void v0_store(const float (&v0r)[3], float *v0, int d) {
+    const int c = ctid();
+    if (cwave() < 0) return;
+#pragma unroll
+    for (int j = 0; j < 3; j++)
+        if (c + NCT * j < d) v0[pad(c + NCT * j)] = v0r[j];
 }
 
 template <int TYPE>
-__device__ __forceinline__ void side_compute(const Side<TYPE> &S, const MegaArgs &a, const MegaLayer *ls, int l,
-                                             int q0, int q1, int o0, int o1, int nbd, int pos, const float *xs,
-                                             float *xn, const float *v0, float *red) {
-    const int lane = tid() & 63;
-    const int d = a.d;
-    {
-        layernorm(xs, xn, d, S.p1, red);
-        float out[SQ];
-        row_dots<TYPE, SQ, 1>(S.pq, nbd, q0, q1, xn, out);
-        const float v = pick<SQ>(out, lane);
-        const int r = lane_row<SQ>(q0, q1);
-        // rows [0,d) q (unused under the reference mask), [d,2d) k, [2d,3d) v
-        if (r >= d) {
-            const int j = r % d, hh = j / 64, c = j % 64;
-            const bool isv = r >= 2 * d;  // S.qb holds this lane's v bias then
-            gfw *kv = glob<gfw>(ls[l].kv);
-            kv[(isv ? (size_t)a.H * a.ctx * 64 : 0) + (size_t)hh * a.ctx * 64 + (size_t)pos * 64 + c] =
-                isv ? v + S.qb : v;
-        }
+__device__ __forceinline__ void b1_prefetch(B1Pre<TYPE> &S, const MegaArgs &a, const MegaLayer *ls, int l, bool item,
+                                            int cq0, int cq1, int q0, int q1, int o0, int o1, int nbd) {
+    const MegaLayer &Ly = ls[l];
+    if (item) {
+        S.qb = lane_bias<SQ>(glob<gf>(Ly.cqb), cq0, cq1);
+        prefetch<TYPE, SQ, 1, SCQ>(S.pq, uview(Ly.cq), nbd, cq0, cq1);
+        prefetch<TYPE, SO, 1, 0>(S.po, uview(Ly.so), nbd, 0, 0);
+        S.ob = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 3; j++) S.v0r[j] = 0.0f;
+        return;
     }
     {
-        __syncthreads();  // v0 complete
-        float out[SO];
-        row_dots<TYPE, SO, 1>(S.po, nbd, o0, o1, v0, out);
-        const float v = pick<SO>(out, lane);
-        const int r = lane_row<SO>(o0, o1);
-        if (r >= 0 && l + 1 < a.L) st_f(&a.sa[(size_t)((l + 1) & 1) * d + r], v + S.ob);
+        // v rows take the v bias; k rows have none; q rows are not used
+        const int lane = tid() & 63, cw = max(cwave(), 0);
+        const int r = max(min(q0 + cw + NC * min(lane, SQ - 1), q1 - 1), 0);
+        S.qb = cwave() >= 0 ? glob<gf>(Ly.svb)[max(r - 2 * a.d, 0)] : 0.0f;
     }
+    // the last layer has no next layer: its own rows are loaded and not used
+    const MegaLayer &Ln = ls[min(l + 1, a.L - 1)];
+    S.ob = lane_bias<SO>(glob<gf>(Ln.sob), o0, o1);
+    v0_load<TYPE>(S.v0r, a, Ln);
+    // the rows last: the first wait for the LN parameters then leaves them in flight
+    prefetch<TYPE, SQ, 1>(S.pq, uview(Ly.sqkv), nbd, q0, q1);
+    prefetch<TYPE, SO, 1>(S.po, uview(Ln.so), nbd, o0, o1);
 }
 
 // Stage K rows [t0, t1) of head ih (a [enc_len][64] block of crossK) into LDS
 // kst in the same layout with direct global->LDS loads (1 KiB per wave
-// instruction), issued by waves 1.. only: wave 0 polls flags and its vector
-// memory counter must stay free of long loads.
+// instruction), issued by the compute waves before the weight rows of the
+// next phase: the first wait for those rows then also covers K.
 __device__ __forceinline__ void stage_k(const float *crossK, int enc_len, int ih, int t0, int t1, float *kst) {
-    const int wave = uni(tid() >> 6), lane = tid() & 63;
-    if (wave == 0) return;
+    const int cw = cwave(), lane = tid() & 63;
+    if (cw < 0) return;
     const float *src = crossK + ((size_t)ih * enc_len + t0) * 64;
     const int nvec = (t1 - t0) * 16;  // 16-byte vectors
     const int nblk = (nvec + 63) / 64;
-    for (int b = wave - 1; b < nblk; b += NW - 1) {
+    for (int b = cw; b < nblk; b += NC) {
         const int v = b * 64 + lane;
         if (v < nvec)
             __builtin_amdgcn_global_load_lds((void __attribute__((address_space(1))) *)(src + 4 * v),
@@ -581,30 +649,38 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
     const int d36 = nbd * 36;
     MegaLayer *ls = (MegaLayer *)lds;     // [L] layer descriptors
     float *xs = lds + layer_floats(L);    // [d36] x_l, later x2 (padded)
-    float *x1s = xs + d36;                // [d36] x1 = x_l + sa_l (item), or V0 of the next layer (side)
-    float *v0 = x1s;
-    float *xn = x1s + d36;                // [4 d36] normalised / staged vectors (padded)
+    float *v0 = xs + d36;                 // [d36] V0 of the next layer (side workgroups)
+    float *xn = v0 + d36;                 // [4 d36] normalised / exchanged vectors (padded)
     float *sav = xn + 4 * d36;            // [d] sa_l (plain)
     float *xl_own = sav + d;              // [64] own rows of x_l
     float *x2_own = xl_own + 64;          // [64] own rows of x2
     float *red = x2_own + 64;             // [64]
     float *qh = red + 64;                 // [64] q of this workgroup's head
-    float *sc = qh + 64;                  // [32*PKV] scores of this workgroup's chunk
+    float *obv = qh + 64;                 // [OUTBOX] posted values
+    int *obi = (int *)(obv + OUTBOX);     // [OUTBOX] posted rows
+    float *xp = (float *)(obi + OUTBOX);  // [64 * XT] a head's chunk sums (leader), argmax partials
+    int *hl = (int *)(xp + 64 * XT);      // [128] the last 128 tokens of the history, by position mod 128
+    float *sc = (float *)(hl + 128);      // [32*PKV] scores of this workgroup's chunk
     int *pen = (int *)(sc + 32 * PKV);    // [pen_floats] window counts of this workgroup's vocabulary rows
     float *kst = (float *)pen + pen_floats(a.V, gridDim.x);  // [chunk_len * 64] K rows of this item's chunk
-    __shared__ unsigned last_flag;
+    __shared__ float eotv;
+    __shared__ int eotf;
 
     {
         const uint32_t *src = (const uint32_t *)a.layers;
         uint32_t *dst = (uint32_t *)ls;
         const int nw = L * (int)(sizeof(MegaLayer) / 4);
         for (int i = tid(); i < nw; i += NT) dst[i] = src[i];
+        // the history the host wrote before the launch; later tokens are appended here
+        for (int i = tid(); i < 128; i += NT) {
+            const int p = a.len0 - 128 + i;
+            if (p >= 0) hl[p & 127] = a.hist[p];
+        }
         __syncthreads();
     }
     const Role &rl = a.roles[w];
     const int item = uni(rl.item), q0 = uni(rl.q0), q1 = uni(rl.q1), o0 = uni(rl.o0), o1 = uni(rl.o1);
     const bool has_item = item >= 0;
-    const bool has_side = q1 > q0 || o1 > o0;
     const int ih = has_item ? item / a.C : 0, ic = has_item ? item % a.C : 0;
     const int t0 = ic * a.chunk_len, t1 = min(t0 + a.chunk_len, a.enc_len);
     // this item's share of its head's cross-query rows
@@ -612,25 +688,28 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
     const int rd0 = (int)((long)w * d / W), rd1 = (int)((long)(w + 1) * d / W);
     const int rf0 = (int)((long)w * 4 * d / W), rf1 = (int)((long)(w + 1) * 4 * d / W);
     const int rv0 = (int)((long)w * a.V / W), rv1 = (int)((long)(w + 1) * a.V / W);
-    unsigned *iflags = a.flags + (size_t)W * FS;  // [H*C] item flags after the workgroup flags
 
     unsigned g = a.g0;
     int tok = a.tok0, len = a.len0, prev = a.prev0, streak = a.streak0;
     int produced = 0;
+
+    // Rows loaded a phase ahead by the compute waves: the S rows (this layer-0
+    // self-attention output rows and V0) and the B1 rows of layer 0.
+    Pre<TYPE, SO> pS;
+    float obS, v0S[3];
+    B1Pre<TYPE> nb1;
+    v0_load<TYPE>(v0S, a, ls[0]);
+    obS = lane_bias<SO>(glob<gf>(ls[0].sob), o0, o1);
+    prefetch<TYPE, SO, 1>(pS, uview(ls[0].so), nbd, o0, o1);
+    if (has_item) stage_k(ls[0].crossK, a.enc_len, ih, t0, t1, kst);
+    b1_prefetch<TYPE>(nb1, a, ls, 0, has_item, cq0, cq1, q0, q1, o0, o1, nbd);
 
     for (int step = 0; step < a.n_steps; step++) {
         const int pos = len - 1;
         // ---------------- S: embedding, sa_0 rows ----------------
         {
             TRACE(step, 0, 7, 0);
-            const int lane = tid() & 63, wave = tid() >> 6;
-            Pre<TYPE, SO> po;
-            prefetch<TYPE, SO, 1>(po, uview(ls[0].so), nbd, o0, o1);
-            const float ob = lane_bias<SO>(glob<gf>(ls[0].sob), o0, o1);
-            {
-                gf *kv = glob<gf>(ls[0].kv) + (size_t)H * a.ctx * 64;
-                for (int i = tid(); i < d; i += NT) v0[pad(i)] = kv[(size_t)(i / 64) * a.ctx * 64 + (i % 64)];
-            }
+            v0_store(v0S, v0, d);
             // token + positional embedding (decoder.go:756-773; quantised rows dequantised bit-exactly)
             for (int i = tid(); i < d; i += NT)
                 xs[pad(i)] = dequant_elem<TYPE>(a.tok, tok, i >> 5, i & 31) + a.pos_emb[(size_t)pos * d + i];
@@ -638,71 +717,113 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
             for (int i = rd0 + tid(); i < rd1; i += NT) xl_own[i - rd0] = xs[pad(i)];
             {
                 float out[SO];
-                row_dots<TYPE, SO, 1>(po, nbd, o0, o1, v0, out);
-                const float v = pick<SO>(out, lane);
-                const int r = lane_row<SO>(o0, o1);
-                if (r >= 0) st_f(&a.sa[r], v + ob);
+                row_dots<TYPE, SO, 1>(pS, nbd, o0, o1, v0, out);
+                post<SO>(obi, obv, lane_row<SO>(o0, o1), pick<SO>(out) + obS);
             }
+            __syncthreads();
             TRACE(step, 0, 7, 2);
-            publish(a.flags, w, ++g);
-            if (has_item) stage_k(ls[0].crossK, a.enc_len, ih, t0, t1, kst);
+            ++g;
+            if (comm()) flush<SO>(obi, obv, a.sa, g);
         }
         for (int l = 0; l < L; l++) {
-            const unsigned gin = g;  // x_l complete when every workgroup flag reaches gin
+            // layer 0: sa_0 carries phase gin (x_0 is local); later layers: x_l carries gin
+            const unsigned gin = g;
+            const MegaLayer &Ly = ls[l];
+            float4 vr[PVK];          // V rows of this item's chunk (C), loaded after B1's dots
+            Pre<TYPE, SD> pd;        // D's rows, loaded after C (items) or B1 (side)
+            float cb;
             // ---------------- B1: cross q rows (items) / side rows ----------------
-            {
-                const int lane = tid() & 63;
-                TRACE(step, l, 1, 0);
-                const MegaLayer &Ly = ls[l];
-                if (has_item) {
-                    Pre<TYPE, SCQ> pc;
-                    LnPar p2;
-                    prefetch<TYPE, SCQ, 1>(pc, uview(Ly.cq), nbd, cq0, cq1);
-                    ln_load(p2, glob<gf>(Ly.ln2w), glob<gf>(Ly.ln2b), d);
-                    const float qb = lane_bias<SCQ>(glob<gf>(Ly.cqb), cq0, cq1);
-                    wait_flags(a.flags, 0, W, gin, a.err);
-                    TRACE(step, l, 1, 1);
-                    if (l > 0) xload_pad(xs, a.xg, d);
-                    else xload(sav, a.sa, d);
-                    __syncthreads();
-                    for (int i = tid(); i < d; i += NT) x1s[pad(i)] = xs[pad(i)] + sav[i];
-                    __syncthreads();
-                    TRACE(step, l, 1, 3);
-                    layernorm(x1s, xn, d, p2, red);
-                    TRACE(step, l, 1, 4);
-                    float out[SCQ];
-                    row_dots<TYPE, SCQ, 1>(pc, nbd, cq0, cq1, xn, out);
-                    const int r = lane_row<SCQ>(cq0, cq1);
-                    if (r >= 0) st_f(&a.qx[r], pick<SCQ>(out, lane) + qb);
-                    TRACE(step, l, 1, 2);
-                    publish(iflags, item, ++g);
+            TRACE(step, l, 1, 0);
+            if (comm()) {
+                // x_l (x_0 is local) and, for items, x1 = x_l + sa_l, LayerNormed into xn:
+                // LN2 for items, LN1 for side workgroups
+                LnW<XD> lp;
+                if (has_item) ln_params<XD>(lp, glob<gf>(Ly.ln2w), glob<gf>(Ly.ln2b), d);
+                else ln_params<XD>(lp, glob<gf>(Ly.ln1w), glob<gf>(Ly.ln1b), d);
+                if (l > 0) {
+                    if (has_item) ll_load_ln<XD, true>(xn, a.xg, d, gin, a.err, lp, sav);
+                    else ll_load_ln<XD, false>(xn, a.xg, d, gin, a.err, lp, nullptr);
                 } else {
-                    Side<TYPE> S;
-                    side_prefetch<TYPE>(S, a, ls, l, q0, q1, o0, o1, nbd, v0);
-                    wait_flags(a.flags, 0, W, gin, a.err);
-                    TRACE(step, l, 1, 1);
-                    if (l > 0) xload_pad(xs, a.xg, d);
-                    else xload(sav, a.sa, d);  // for D's x1 rows
-                    __syncthreads();
-                    side_compute<TYPE>(S, a, ls, l, q0, q1, o0, o1, nbd, pos, xs, xn, v0, red);
-                    TRACE(step, l, 1, 2);
-                    ++g;
+                    ll_load<XD, false>(sav, a.sa, d, gin, a.err);
+                    const int lane = tid() & 63;
+                    float x[XD];
+#pragma unroll
+                    for (int k = 0; k < XD; k++) {
+                        const int i = min(lane + 64 * k, d - 1);
+                        x[k] = has_item ? xs[pad(i)] + sav[i] : xs[pad(i)];
+                    }
+                    ln_wave<XD>(x, d, lp, xn);
                 }
+                TRACE(step, l, 1, 1);
+            } else if (!has_item) {
+                v0_store(nb1.v0r, v0, d);
             }
-            const unsigned gB1 = g;
+            __syncthreads();
+            ++g;
+            const unsigned gB1 = g;  // items' cross-query rows; side workgroups' sa_{l+1} rows
+            if (has_item) {
+                {
+                    float out[SQ];
+                    row_dots<TYPE, SQ, 1>(nb1.pq, nbd, cq0, cq1, xn, out);
+                    post<SQ>(obi, obv, lane_row<SQ>(cq0, cq1), pick<SQ>(out) + nb1.qb);
+                }
+                __syncthreads();
+                TRACE(step, l, 1, 2);
+                if (comm()) flush<SQ>(obi, obv, a.qx, gB1);
+                {
+                    // C's V rows (zeros in the communication wave)
+                    gf *Vv = glob<gf>(Ly.crossV) + (size_t)ih * a.enc_len * 64;
+                    const int c = ctid();
+                    const bool cwv = cwave() >= 0;
+#pragma unroll
+                    for (int j = 0; j < PVK; j++) {
+                        const int t = min(t0 + (j * NCT + c) / 16, t1 - 1);
+                        vr[j] = cwv ? ld16f(Vv + (unsigned)t * 64u + 4u * (unsigned)(c & 15))
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+                    }
+                }
+                prefetch<TYPE, SD, 1, 0>(pd, uview(Ly.co), nbd, 0, 0);  // zeros until C
+                cb = 0.0f;
+            } else {
+                {
+                    float out[SQ];
+                    row_dots<TYPE, SQ, 1>(nb1.pq, nbd, q0, q1, xn, out);
+                    const float v = pick<SQ>(out);
+                    const int r = lane_row<SQ>(q0, q1);
+                    // rows [0,d) q (unused under the reference mask), [d,2d) k, [2d,3d) v; the
+                    // cache rows are read only after the launch, so the compute lanes store them
+                    if (r >= d) {
+                        const int j = r % d, hh = j / 64, cidx = j % 64;
+                        const bool isv = r >= 2 * d;  // nb1.qb holds this lane's v bias then
+                        gfw *kv = glob<gfw>(Ly.kv);
+                        kv[(isv ? (size_t)H * a.ctx * 64 : 0) + (size_t)hh * a.ctx * 64 + (size_t)pos * 64 + cidx] =
+                            isv ? v + nb1.qb : v;
+                    }
+                }
+                {
+                    float out[SO];
+                    row_dots<TYPE, SO, 1>(nb1.po, nbd, o0, o1, v0, out);
+                    post<SO>(obi, obv, l + 1 < L ? lane_row<SO>(o0, o1) : -1, pick<SO>(out) + nb1.ob);
+                }
+                __syncthreads();
+                TRACE(step, l, 1, 2);
+                // sa_{l+1}, read in F of this layer
+                if (comm()) flush<SO>(obi, obv, a.sa + (size_t)((l + 1) & 1) * d, gB1);
+#pragma unroll
+                for (int j = 0; j < PVK; j++) vr[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                // D's rows (B2 and C are item work)
+                prefetch<TYPE, SD, 1>(pd, uview(Ly.co), nbd, rd0, rd1);
+                cb = lane_bias<SD>(glob<gf>(Ly.cob), rd0, rd1);
+            }
             // ---------------- B2: scores of the chunk against the head's q ----------------
             ++g;
             const unsigned gB = g;
             if (has_item) {
                 const int lane = tid() & 63, wave = tid() >> 6;
                 TRACE(step, l, 0, 0);
-                wait_flags(iflags, ih * a.C, a.C, gB1, a.err);
-                TRACE(step, l, 0, 1);
-                if (tid() < 32) {
-                    const uint64_t v = __hip_atomic_load((const uint64_t *)(a.qx + ih * 64) + tid(), __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-                    *(float2 *)&qh[2 * tid()] =
-                        make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+                if (comm()) {
+                    ll_load<1, false>(qh, a.qx + ih * 64, 64, gB1, a.err);
+                    TRACE(step, l, 0, 1);
                 }
                 __syncthreads();
                 const float4 q4 = ((const float4 *)qh)[tid() & 15];
@@ -724,265 +845,266 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 mx = wave_max(mx);
                 if (lane == 0) red[wave] = mx;
                 __syncthreads();
-                if (tid() == 0) {
+                TRACE(step, l, 0, 2);
+                if (comm() && tid() == 0) {
                     float m = red[0];
                     for (int i = 1; i < NW; i++) m = fmaxf(m, red[i]);
-                    st_f(&a.cmax[item], m);
+                    st_pair(&a.cmax[item], m, gB);
                 }
-                TRACE(step, l, 0, 2);
-                publish(iflags, item, gB);
             }
             // ---------------- C: softmax weights, partial P.V, head combine ----------------
             ++g;
             const unsigned gC = g;
             if (has_item) {
-                const int lane = tid() & 63, wave = tid() >> 6;
+                const int lane = tid() & 63, cw = cwave();
                 TRACE(step, l, 2, 0);
-                const MegaLayer &Ly = ls[l];
-                float4 vr[PKV];
-                gf *Vv = glob<gf>(Ly.crossV) + (size_t)ih * a.enc_len * 64;
-                const int tt = tid();
-#pragma unroll
-                for (int j = 0; j < PKV; j++) {
-                    const int t = min(t0 + (j * NT + tt) / 16, t1 - 1);
-                    vr[j] = ld16f(Vv + (unsigned)t * 64u + 4u * (unsigned)(tt & 15));
-                }
-                wait_flags(iflags, ih * a.C, a.C, gB, a.err);
-                TRACE(step, l, 2, 1);
-                // chunk maxima of the head: all loads in flight before the first use
-                float cm[CMAX];
-#pragma unroll
-                for (int i = 0; i < CMAX; i++) cm[i] = i < a.C ? ld_f(&a.cmax[ih * a.C + i]) : -INFINITY;
-                float M = cm[0];
-#pragma unroll
-                for (int i = 1; i < CMAX; i++) M = fmaxf(M, cm[i]);
-                float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-                float es = 0.0f;
-#pragma unroll
-                for (int j = 0; j < PKV; j++) {
-                    const int t = t0 + (j * NT + tid()) / 16;
-                    if (t < t1) {
-                        const float e = fast_exp(sc[t - t0] - M);
-                        acc.x += e * vr[j].x; acc.y += e * vr[j].y; acc.z += e * vr[j].z; acc.w += e * vr[j].w;
-                        if ((tid() & 15) == 0) es += e;
-                    }
-                }
-#pragma unroll
-                for (int o = 16; o < 64; o <<= 1) {
-                    acc.x += __shfl_xor(acc.x, o, 64);
-                    acc.y += __shfl_xor(acc.y, o, 64);
-                    acc.z += __shfl_xor(acc.z, o, 64);
-                    acc.w += __shfl_xor(acc.w, o, 64);
-                }
-                es = wave_sum(es);
-                float4 *red4 = (float4 *)xn;  // [NW][16]
-                if (lane < 16) red4[wave * 16 + lane] = acc;
-                if (lane == 0) red[wave] = es;
-                __syncthreads();
-                float *pv = a.parts + (size_t)item * 65;
-                if (tid() < 16) {
-                    float4 r = red4[tid()];
-                    for (int v2 = 1; v2 < NW; v2++) {
-                        const float4 t4 = red4[v2 * 16 + tid()];
-                        r.x += t4.x; r.y += t4.y; r.z += t4.z; r.w += t4.w;
-                    }
-                    st_f(&pv[4 * tid()], r.x);
-                    st_f(&pv[4 * tid() + 1], r.y);
-                    st_f(&pv[4 * tid() + 2], r.z);
-                    st_f(&pv[4 * tid() + 3], r.w);
-                }
-                if (tid() == 0) {
-                    float s = 0.0f;
-                    for (int v2 = 0; v2 < NW; v2++) s += red[v2];
-                    st_f(&pv[64], s);
-                }
-                __builtin_amdgcn_s_waitcnt(0);
-                __syncthreads();
-                // the last chunk of this head to arrive combines the head
-                if (tid() == 0) {
-                    const unsigned old = __hip_atomic_fetch_add(&a.hcount[(size_t)(l * H + ih) * FS], 1u,
-                                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    last_flag = ((old + 1) % (unsigned)a.C) == 0;
+                if (comm()) {
+                    // chunk maxima of the head
+                    ll_load<1, false>(red + 40, a.cmax + ih * a.C, a.C, gB, a.err);
+                    TRACE(step, l, 2, 1);
+                    float M = red[40];
+                    for (int i = 1; i < a.C; i++) M = fmaxf(M, red[40 + i]);
+                    if (lane == 0) red[32] = M;
                 }
                 __syncthreads();
-                if (last_flag && tid() < 64) {
-                    float ps[CMAX], po[CMAX];
+                if (cw >= 0) {
+                    const float M = red[32];
+                    const int c = ctid();
+                    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+                    float es = 0.0f;
 #pragma unroll
-                    for (int i = 0; i < CMAX; i++) {
-                        const float *p2 = a.parts + (size_t)(ih * a.C + min(i, a.C - 1)) * 65;
-                        ps[i] = i < a.C ? ld_f(&p2[64]) : 0.0f;
-                        po[i] = i < a.C ? ld_f(&p2[tid()]) : 0.0f;
+                    for (int j = 0; j < PVK; j++) {
+                        const int t = t0 + (j * NCT + c) / 16;
+                        if (t < t1) {
+                            const float e = fast_exp(sc[t - t0] - M);
+                            acc.x += e * vr[j].x; acc.y += e * vr[j].y; acc.z += e * vr[j].z; acc.w += e * vr[j].w;
+                            if ((c & 15) == 0) es += e;
+                        }
                     }
-                    float sum = 0.0f, o = 0.0f;
 #pragma unroll
-                    for (int i = 0; i < CMAX; i++) {
-                        sum += ps[i];
-                        o += po[i];
+                    for (int o = 16; o < 64; o <<= 1) {
+                        acc.x += __shfl_xor(acc.x, o, 64);
+                        acc.y += __shfl_xor(acc.y, o, 64);
+                        acc.z += __shfl_xor(acc.z, o, 64);
+                        acc.w += __shfl_xor(acc.w, o, 64);
                     }
-                    st_f(&a.attn[ih * 64 + tid()], o * (1.0f / sum));
-                    __builtin_amdgcn_s_waitcnt(0);
-                    if (tid() == 0) st_u(&a.hflags[(size_t)ih * FS], gC);
+                    es = wave_sum(es);
+                    float4 *red4 = (float4 *)xn;  // [NC][16]
+                    if (lane < 16) red4[cw * 16 + lane] = acc;
+                    if (lane == 0) red[cw] = es;
                 }
-                TRACE(step, l, 2, 2);
-                if (has_side) {
-                    // fewer side workgroups than the side rows need: items take a share after C
-                    __syncthreads();
-                    Side<TYPE> S;
-                    side_prefetch<TYPE>(S, a, ls, l, q0, q1, o0, o1, nbd, v0);
-                    __syncthreads();
-                    side_compute<TYPE>(S, a, ls, l, q0, q1, o0, o1, nbd, pos, xs, xn, v0, red);
+                __syncthreads();
+                if (cw >= 0) {
+                    // D's rows, while the communication wave combines
+                    prefetch<TYPE, SD, 1>(pd, uview(Ly.co), nbd, rd0, rd1);
+                    cb = lane_bias<SD>(glob<gf>(Ly.cob), rd0, rd1);
+                } else {
+                    const float4 *red4 = (const float4 *)xn;
+                    uint64_t *pv = a.parts + (size_t)item * 65;
+                    if (lane < 16) {
+                        float4 r = red4[lane];
+                        for (int v2 = 1; v2 < NC; v2++) {
+                            const float4 t4 = red4[v2 * 16 + lane];
+                            r.x += t4.x; r.y += t4.y; r.z += t4.z; r.w += t4.w;
+                        }
+                        st_pair(&pv[4 * lane], r.x, gC);
+                        st_pair(&pv[4 * lane + 1], r.y, gC);
+                        st_pair(&pv[4 * lane + 2], r.z, gC);
+                        st_pair(&pv[4 * lane + 3], r.w, gC);
+                    }
+                    if (lane == 0) {
+                        float s = 0.0f;
+                        for (int v2 = 0; v2 < NC; v2++) s += red[v2];
+                        st_pair(&pv[64], s, gC);
+                    }
+                    if (ic == 0) {
+                        // the head's first chunk combines the head: sum of the chunks' weight sums and P.V
+                        ll_load<XP, false>(xp, a.parts + (size_t)ih * a.C * 65, a.C * 65, gC, a.err);
+                        float sum = 0.0f, o = 0.0f;
+                        for (int i = 0; i < a.C; i++) {
+                            sum += xp[i * 65 + 64];
+                            o += xp[i * 65 + lane];
+                        }
+                        st_pair(&a.attn[ih * 64 + lane], o * (1.0f / sum), gC);
+                    }
+                    TRACE(step, l, 2, 2);
                 }
             }
             // ---------------- D: cross out rows -> x2 ----------------
+            Pre<TYPE, SE> pe;
+            float fbE;
             {
-                const int lane = tid() & 63, wave = tid() >> 6;
                 TRACE(step, l, 3, 0);
-                const MegaLayer &Ly = ls[l];
-                Pre<TYPE, SD> pd;
-                prefetch<TYPE, SD, 1>(pd, uview(Ly.co), nbd, rd0, rd1);
-                const float cb = lane_bias<SD>(glob<gf>(Ly.cob), rd0, rd1);
-                wait_flags(a.hflags, 0, H, gC, a.err);
-                TRACE(step, l, 3, 1);
-                xload_pad(xn, a.attn, d);
+                if (comm()) {
+                    ll_load<XD, true>(xn, a.attn, d, gC, a.err);
+                    TRACE(step, l, 3, 1);
+                }
                 __syncthreads();
                 {
                     float out[SD];
                     row_dots<TYPE, SD, 1>(pd, nbd, rd0, rd1, xn, out);
-                    const float v = pick<SD>(out, lane);
+                    const float v = pick<SD>(out);
                     const int r = lane_row<SD>(rd0, rd1);
+                    float x2 = 0.0f;
                     if (r >= 0) {
                         const float x1 = xl_own[r - rd0] + sav[r];
-                        const float x2 = x1 + (v + cb);
+                        x2 = x1 + (v + cb);
                         x2_own[r - rd0] = x2;
-                        st_f(&a.x2[r], x2);
                     }
+                    post<SD>(obi, obv, r, x2);
                 }
+                __syncthreads();
                 TRACE(step, l, 3, 2);
-                publish(a.flags, w, ++g);
+                ++g;
+                if (comm()) flush<SD>(obi, obv, a.x2, g);
+                // E's bias and rows
+                fbE = lane_bias<SE>(glob<gf>(Ly.fc1b), rf0, rf1);
+                prefetch<TYPE, SE, 1>(pe, uview(Ly.fc1), nbd, rf0, rf1);
             }
             const unsigned gD = g;
             // ---------------- E: LN3 + fc1 + GELU ----------------
+            Pre<TYPE, SD * PFC2> pf;
+            float fbF;
             {
-                const int lane = tid() & 63, wave = tid() >> 6;
                 TRACE(step, l, 4, 0);
-                const MegaLayer &Ly = ls[l];
-                Pre<TYPE, SE> pe;
-                LnPar p3;
-                prefetch<TYPE, SE, 1>(pe, uview(Ly.fc1), nbd, rf0, rf1);
-                const float fb = lane_bias<SE>(glob<gf>(Ly.fc1b), rf0, rf1);
-                ln_load(p3, glob<gf>(Ly.ln3w), glob<gf>(Ly.ln3b), d);
-                wait_flags(a.flags, 0, W, gD, a.err);
-                TRACE(step, l, 4, 1);
-                xload_pad(xs, a.x2, d);
+                if (comm()) {
+                    LnW<XD> lp;
+                    ln_params<XD>(lp, glob<gf>(Ly.ln3w), glob<gf>(Ly.ln3b), d);
+                    ll_load_ln<XD, false>(xn, a.x2, d, gD, a.err, lp, nullptr);
+                    TRACE(step, l, 4, 1);
+                }
                 __syncthreads();
                 TRACE(step, l, 4, 3);
-                layernorm(xs, xn, d, p3, red);
                 TRACE(step, l, 4, 4);
+                TRACEC(step, l, 4, 7);
                 {
                     float out[SE];
                     row_dots<TYPE, SE, 1>(pe, nbd, rf0, rf1, xn, out);
-                    TRACE(step, l, 4, 5);
-                    const float v = pick<SE>(out, lane);
+                    TRACEC(step, l, 4, 5);
+                    const float v = pick<SE>(out);
                     const int r = lane_row<SE>(rf0, rf1);
-                    if (r >= 0) st_f(&a.hbuf[r], gelu_ref(v + fb));
+                    post<SE>(obi, obv, r, r >= 0 ? gelu_f32(v + fbE) : 0.0f);
                 }
+                __syncthreads();
                 TRACE(step, l, 4, 2);
-                publish(a.flags, w, ++g);
+                ++g;
+                if (comm()) flush<SE>(obi, obv, a.hbuf, g);
+                TRACE(step, l, 4, 6);
+                // F's bias and rows
+                fbF = lane_bias<SD>(glob<gf>(Ly.fc2b), rd0, rd1);
+                prefetch<TYPE, SD * PFC2, PFC2>(pf, uview(Ly.fc2), nbf, rd0, rd1);
             }
             const unsigned gE = g;
             // ---------------- F: fc2 rows -> x_{l+1} ----------------
             {
-                const int lane = tid() & 63, wave = tid() >> 6;
                 TRACE(step, l, 5, 0);
-                const MegaLayer &Ly = ls[l];
-                Pre<TYPE, SD * PFC2> pf;
-                prefetch<TYPE, SD * PFC2, PFC2>(pf, uview(Ly.fc2), nbf, rd0, rd1);
-                const float fb = lane_bias<SD>(glob<gf>(Ly.fc2b), rd0, rd1);
-                // the next layer's K chunk (this layer's was consumed in B2)
-                if (has_item && l + 1 < L) stage_k(ls[l + 1].crossK, a.enc_len, ih, t0, t1, kst);
-                wait_flags(a.flags, 0, W, gE, a.err);
+                // h by the compute waves (12 pairs per lane), sa_{l+1} by the communication wave
+                if (comm()) {
+                    if (l + 1 < L) ll_load<XD, false>(sav, a.sa + (size_t)((l + 1) & 1) * d, d, gB1, a.err);
+                } else {
+                    ll_load<XH, true>(xn, a.hbuf, 4 * d, gE, a.err, cwave() * 64 * XH);
+                }
                 TRACE(step, l, 5, 1);
-                xload_pad(xn, a.hbuf, 4 * d);
-                if (l + 1 < L) xload(sav, a.sa + (size_t)((l + 1) & 1) * d, d);
                 __syncthreads();
                 TRACE(step, l, 5, 3);
                 {
                     float out[SD];
                     row_dots<TYPE, SD * PFC2, PFC2>(pf, nbf, rd0, rd1, xn, out);
-                    TRACE(step, l, 5, 5);
-                    const float v = pick<SD>(out, lane);
+                    TRACEC(step, l, 5, 5);
+                    const float v = pick<SD>(out);
                     const int r = lane_row<SD>(rd0, rd1);
+                    float x = 0.0f;
                     if (r >= 0) {
-                        const float x = x2_own[r - rd0] + (v + fb);
+                        x = x2_own[r - rd0] + (v + fbF);
                         xl_own[r - rd0] = x;
-                        st_f(&a.xg[r], x);
                     }
+                    post<SD>(obi, obv, r, x);
                 }
+                __syncthreads();
                 TRACE(step, l, 5, 2);
-                publish(a.flags, w, ++g);
+                ++g;
+                if (comm()) flush<SD>(obi, obv, a.xg, g);
+                TRACE(step, l, 5, 6);
+                if (l + 1 < L) {
+                    // the next layer's K chunk (this layer's was consumed in B2), then its B1 rows
+                    if (has_item) stage_k(ls[l + 1].crossK, a.enc_len, ih, t0, t1, kst);
+                    b1_prefetch<TYPE>(nb1, a, ls, l + 1, has_item, cq0, cq1, q0, q1, o0, o1, nbd);
+                }
             }
         }
         const unsigned gF = g;
         // ---------------- T: final LN, logits rows, penalty, argmax ----------------
         {
-            const int lane = tid() & 63, wave = tid() >> 6;
+            const int lane = tid() & 63, cw = cwave();
             TRACE(step, L, 6, 0);
             const UView vt = uview(a.tok);
             Pre<TYPE, TS> p0, p1;
             const int CH = NC * TS;
-            LnPar pf;
             prefetch<TYPE, TS, 1>(p0, vt, nbd, rv0, min(rv0 + CH, rv1));
-            ln_load(pf, glob<gf>(a.lnw), glob<gf>(a.lnb), d);
-            for (int i = tid(); i < rv1 - rv0; i += NT) pen[i] = 0;
-            wait_flags(a.flags, 0, W, gF, a.err);
-            TRACE(step, L, 6, 1);
-            xload_pad(xs, a.xg, d);
-            // repetition window (decoder.go:1000-1016): counts of this workgroup's rows
-            const int start = len > 128 ? len - 128 : 0, nwin = len - start;
-            if (tid() < nwin) {
-                const int id = (int)ld_u((const unsigned *)&a.hist[start + tid()]);
-                if (id >= rv0 && id < rv1) atomicAdd(&pen[id - rv0], 1);
+            if (comm()) {
+                for (int i = tid(); i < rv1 - rv0; i += 64) pen[i] = 0;
+                if (tid() == 0) eotf = 0;
+                // repetition window (decoder.go:1000-1016): counts of this workgroup's rows
+                const int start = len > 128 ? len - 128 : 0, nwin = len - start;
+                for (int i = tid(); i < nwin; i += 64) {
+                    const int id = hl[(start + i) & 127];
+                    if (id >= rv0 && id < rv1) atomicAdd(&pen[id - rv0], 1);
+                }
+                LnW<XD> lp;
+                ln_params<XD>(lp, glob<gf>(a.lnw), glob<gf>(a.lnb), d);
+                ll_load_ln<XD, false>(xn, a.xg, d, gF, a.err, lp, nullptr);
+                TRACE(step, L, 6, 1);
             }
             __syncthreads();
             TRACE(step, L, 6, 3);
-            layernorm(xs, xn, d, pf, red);
             TRACE(step, L, 6, 4);
             float bv = -INFINITY, bv2 = -INFINITY;
             int bi = 0x7FFFFFFF, bi2 = 0x7FFFFFFF;
+            float ev = -INFINITY;
             for (int base = rv0; base < rv1; base += 2 * CH) {
                 const int b1 = base + CH;
                 prefetch<TYPE, TS, 1>(p1, vt, nbd, min(b1, rv1 - 1), min(b1 + CH, rv1));
-                logits_chunk<TYPE>(a, p0, nbd, base, min(base + CH, rv1), xn, pen, rv0, bv, bi, bv2, bi2);
+                logits_chunk<TYPE>(a, p0, nbd, base, min(base + CH, rv1), xn, pen, rv0, bv, bi, bv2, bi2, &ev);
                 if (b1 < rv1) {
                     const int b2 = b1 + CH;
                     prefetch<TYPE, TS, 1>(p0, vt, nbd, min(b2, rv1 - 1), min(b2 + CH, rv1));
-                    logits_chunk<TYPE>(a, p1, nbd, b1, min(b1 + CH, rv1), xn, pen, rv0, bv, bi, bv2, bi2);
+                    logits_chunk<TYPE>(a, p1, nbd, b1, min(b1 + CH, rv1), xn, pen, rv0, bv, bi, bv2, bi2, &ev);
                 }
             }
             TRACE(step, L, 6, 5);
             float *rv = red;
-            float *rv2 = red + NW;
-            int *ri = (int *)(red + 2 * NW), *ri2 = (int *)(red + 3 * NW);
-            if (lane == 0) { rv[wave] = bv; ri[wave] = bi; rv2[wave] = bv2; ri2[wave] = bi2; }
-            __syncthreads();
-            if (tid() == 0) {
-                for (int i = 1; i < NW; i++) { better(rv[i], ri[i], rv[0], ri[0]); better(rv2[i], ri2[i], rv2[0], ri2[0]); }
-                st_f(&a.pval[w], rv[0]);
-                st_u((unsigned *)&a.pidx[w], (unsigned)ri[0]);
-                st_f(&a.pval[W + w], rv2[0]);
-                st_u((unsigned *)&a.pidx[W + w], (unsigned)ri2[0]);
+            float *rv2 = red + NC;
+            int *ri = (int *)(red + 2 * NC), *ri2 = (int *)(red + 3 * NC);
+            if (cw >= 0 && lane == 0) {
+                rv[cw] = bv; ri[cw] = bi; rv2[cw] = bv2; ri2[cw] = bi2;
+                if (ev != -INFINITY) {
+                    eotv = ev;
+                    eotf = 1;
+                }
             }
-            TRACE(step, L, 6, 2);
-            publish(a.flags, w, ++g);
-            wait_flags(a.flags, 0, W, g, a.err);
-            TRACE(step, L, 6, 6);
-            // every workgroup reduces the partials the same way
-            if (tid() < 64) {
+            __syncthreads();
+            const unsigned gT = g + 1;
+            if (comm()) {
+                if (tid() == 0) {
+                    for (int i = 1; i < NC; i++) {
+                        better(rv[i], ri[i], rv[0], ri[0]);
+                        better(rv2[i], ri2[i], rv2[0], ri2[0]);
+                    }
+                    st_pair(&a.part[4 * w], rv[0], gT);
+                    st_pair(&a.part[4 * w + 1], __int_as_float(ri[0]), gT);
+                    st_pair(&a.part[4 * w + 2], rv2[0], gT);
+                    st_pair(&a.part[4 * w + 3], __int_as_float(ri2[0]), gT);
+                    if (eotf) st_pair(a.eot_logit, eotv, gT);
+                }
+                TRACE(step, L, 6, 2);
+                ll_load<XT, false>(xp, a.part, 4 * W, gT, a.err);
+                TRACE(step, L, 6, 6);
+                // every workgroup reduces the partials the same way
                 float b1 = -INFINITY, b2 = -INFINITY;
                 int i1 = 0x7FFFFFFF, i2 = 0x7FFFFFFF;
                 for (int i = tid(); i < W; i += 64) {
-                    better(ld_f(&a.pval[i]), (int)ld_u((const unsigned *)&a.pidx[i]), b1, i1);
-                    better(ld_f(&a.pval[W + i]), (int)ld_u((const unsigned *)&a.pidx[W + i]), b2, i2);
+                    better(xp[4 * i], __float_as_int(xp[4 * i + 1]), b1, i1);
+                    better(xp[4 * i + 2], __float_as_int(xp[4 * i + 3]), b2, i2);
                 }
                 for (int o = 32; o > 0; o >>= 1) {
                     float ov = __shfl_xor(b1, o, 64);
@@ -992,20 +1114,29 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                     oi = __shfl_xor(i2, o, 64);
                     better(ov, oi, b2, i2);
                 }
-                if (tid() == 0) {
-                    int id = (i1 == 0x7FFFFFFF) ? 0 : i1;
-                    if (a.suppress_nst && a.eot >= 0 && a.eot < a.V && id == a.eot && ld_f(a.eot_logit) < -a.nst)
-                        id = (i2 == 0x7FFFFFFF) ? a.eot : i2;
-                    red[63] = __int_as_float(id);
+                int id = (i1 == 0x7FFFFFFF) ? 0 : i1;
+                if (a.suppress_nst && a.eot >= 0 && a.eot < a.V && id == a.eot) {
+                    ll_load<1, false>(xp, a.eot_logit, 1, gT, a.err);
+                    if (xp[0] < -a.nst) id = (i2 == 0x7FFFFFFF) ? a.eot : i2;
                 }
+                if (tid() == 0) red[63] = __int_as_float(id);
             }
+            // the next step's S and B1 rows and its first K chunk (the communication
+            // wave, done with its part, fills zeros)
+            v0_load<TYPE>(v0S, a, ls[0]);
+            obS = lane_bias<SO>(glob<gf>(ls[0].sob), o0, o1);
+            prefetch<TYPE, SO, 1>(pS, uview(ls[0].so), nbd, o0, o1);
+            if (has_item) stage_k(ls[0].crossK, a.enc_len, ih, t0, t1, kst);
+            b1_prefetch<TYPE>(nb1, a, ls, 0, has_item, cq0, cq1, q0, q1, o0, o1, nbd);
+            g = gT;
             __syncthreads();
             tok = __float_as_int(red[63]);
             __syncthreads();
         }
         // history append and the reference's stop rules (decoder.go:462-484)
+        if (tid() == 0) hl[len & 127] = tok;
         if (w == 0 && tid() == 0) {
-            st_u((unsigned *)&a.hist[len], (unsigned)tok);
+            a.hist[len] = tok;
             a.out_tokens[produced] = tok;
         }
         len++;
@@ -1033,8 +1164,8 @@ extern "C" int wh_mega_trace_read(void *out, size_t bytes) {
 
 size_t lds_bytes(int d, int L, int V, int W, int chunk_len) {
     const int d36 = ((d + 31) / 32) * 36;
-    return sizeof(float) *
-           (size_t)(layer_floats(L) + 6 * d36 + d + 64 * 4 + 32 * PKV + pen_floats(V, W) + chunk_len * 64);
+    return sizeof(float) * (size_t)(layer_floats(L) + 6 * d36 + d + 64 * 4 + 2 * OUTBOX + 64 * XT + 128 +
+                                    32 * PKV + pen_floats(V, W) + chunk_len * 64);
 }
 
 int launch_decode(uint32_t type, int grid, const MegaArgs &a, hipStream_t st) {

@@ -273,15 +273,22 @@ int mega_setup(wh_seq &s) {
     if (hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, m.device) != hipSuccess)
         return WH_OK;
     const int W = std::min(env_int("WHISPER_HIP_GRID", dev_cus), dev_cus);
-    // C >= CMIN chunks of at most 32*PKV keys; the last chunk is not empty
-    const int C = std::max(mega::CMIN, (s.enc_len + 32 * mega::PKV - 1) / (32 * mega::PKV));
+    // C >= CMIN chunks of at most CHUNK_MAX keys; the last chunk is not empty
+    const int C = std::max(mega::CMIN, (s.enc_len + mega::CHUNK_MAX - 1) / mega::CHUNK_MAX);
     const int chunk = (s.enc_len + C - 1) / C;
-    if (s.enc_len < 16 || (C - 1) * chunk >= s.enc_len || chunk > 32 * mega::PKV) return WH_OK;
+    if (s.enc_len < 16 || (C - 1) * chunk >= s.enc_len || chunk > mega::CHUNK_MAX || chunk > 32 * mega::PKV)
+        return WH_OK;
     const int items = H * C;
-    // per-workgroup row capacities of the kernel's register slots
+    // per-workgroup row capacities of the kernel's register slots (compute waves only)
     auto per = [&](int rows, int n) { return (rows + n - 1) / n; };
-    const int NW = mega::WAVES;
-    if (C > mega::CMAX || W < 8 || items > W || W > 256 || H > 256 || per(d, W) > NW * mega::SD || per(4 * d, W) > NW * mega::SE) return WH_OK;
+    const int NC = mega::CWAVES;
+    // LayerNorm: 3 elements per compute thread; exchange loads: XD, XH, XT, XP pairs per lane
+    if (d > 3 * 64 * NC || d > 64 * mega::XD || 4 * d > 64 * NC * mega::XH || 4 * W > 64 * mega::XT ||
+        mega::CMAX * 65 > 64 * mega::XP)
+        return WH_OK;
+    if (C > mega::CMAX || W < 8 || items >= W || W > 256 || H > 256 || per(d, W) > NC * mega::SD ||
+        per(4 * d, W) > NC * mega::SE || per(64, C) > NC * mega::SCQ || mega::SCQ > mega::SQ)
+        return WH_OK;
     if (mega::lds_bytes(d, L, m.n_vocab, W, chunk) + 64 > (size_t)lds_max) return WH_OK;
     auto fits32 = [](const DevMat &x) { return (uint64_t)x.rows * x.nb * 32 < (1ull << 32); };
     if (!fits32(m.tok)) return WH_OK;
@@ -289,9 +296,7 @@ int mega_setup(wh_seq &s) {
         if (!fits32(l.sqkv) || !fits32(l.so) || !fits32(l.cq) || !fits32(l.co) || !fits32(l.fc1) || !fits32(l.fc2))
             return WH_OK;
     // Roles. Workgroup w runs on XCD w % 8; the chunks of one head go to one
-    // XCD when they fit, so the head's redundant cross-query rows hit that
-    // XCD's L2. Side rows go to the workgroups without an item when they are
-    // enough, otherwise to every workgroup.
+    // XCD when they fit, so their head-local exchanges stay near one L2.
     std::vector<mega::Role> roles(W);
     for (auto &r : roles) r = mega::Role{-1, 0, 0, 0, 0, {0, 0, 0}};
     {
@@ -310,15 +315,12 @@ int mega_setup(wh_seq &s) {
             for (int i = 0; i < items; i++) roles[i].item = i;
         }
     }
+    // the side rows go to the workgroups without an item
     std::vector<int> side;
     for (int w = 0; w < W; w++)
         if (roles[w].item < 0) side.push_back(w);
     const int ns = (int)side.size();
-    if (ns == 0 || per(3 * d, ns) > NW * mega::SQ || per(d, ns) > NW * mega::SO) {
-        side.clear();
-        for (int w = 0; w < W; w++) side.push_back(w);
-    }
-    if (per(3 * d, (int)side.size()) > NW * mega::SQ || per(d, (int)side.size()) > NW * mega::SO) return WH_OK;
+    if (ns == 0 || per(3 * d, ns) > NC * mega::SQ || per(d, ns) > NC * mega::SO) return WH_OK;
     for (size_t j = 0; j < side.size(); j++) {
         const long n = (long)side.size();
         mega::Role &r = roles[side[j]];
@@ -353,19 +355,17 @@ int mega_setup(wh_seq &s) {
     a.tok = view(m.tok);
     a.pos_emb = m.pos; a.lnw = m.lnw; a.lnb = m.lnb;
     a.hist = s.hist;
-    const int FS = mega::FLAG_STRIDE;
 #define MALLOC(p, n) do { if ((rc = s.alloc(&(p), (n)))) return rc; } while (0)
-    MALLOC(a.xg, (size_t)d); MALLOC(a.sa, (size_t)2 * d); MALLOC(a.x2, (size_t)d); MALLOC(a.hbuf, (size_t)4 * d);
-    MALLOC(a.attn, (size_t)d); MALLOC(a.qx, (size_t)d); MALLOC(a.cmax, (size_t)items); MALLOC(a.parts, (size_t)items * 65);
-    MALLOC(a.pval, (size_t)2 * W); MALLOC(a.pidx, (size_t)2 * W); MALLOC(a.eot_logit, 1);
-    // workgroup flags [W] then item flags [items]
-    MALLOC(a.flags, (size_t)(W + items) * FS); MALLOC(a.hflags, (size_t)H * FS);
-    MALLOC(a.hcount, (size_t)L * H * FS);
+    // exchange pairs start at phase 0; the kernel's phases count from g0 + 1
+    const size_t npairs[] = {(size_t)d, (size_t)2 * d, (size_t)d, (size_t)4 * d, (size_t)d, (size_t)d, (size_t)items,
+                             (size_t)items * 65, (size_t)W * 4, 1};
+    uint64_t **pbuf[] = {&a.xg, &a.sa, &a.x2, &a.hbuf, &a.attn, &a.qx, &a.cmax, &a.parts, &a.part, &a.eot_logit};
+    for (int i = 0; i < 10; i++) {
+        MALLOC(*pbuf[i], npairs[i]);
+        WH_HIP(hipMemsetAsync(*pbuf[i], 0, sizeof(uint64_t) * npairs[i], s.st));
+    }
     MALLOC(a.err, 1); MALLOC(a.state_out, 4); MALLOC(a.out_tokens, (size_t)s.hist_cap);
 #undef MALLOC
-    WH_HIP(hipMemsetAsync(a.flags, 0, sizeof(unsigned) * (W + items) * FS, s.st));
-    WH_HIP(hipMemsetAsync(a.hflags, 0, sizeof(unsigned) * H * FS, s.st));
-    WH_HIP(hipMemsetAsync(a.hcount, 0, sizeof(unsigned) * L * H * FS, s.st));
     WH_HIP(hipMemsetAsync(a.err, 0, sizeof(unsigned), s.st));
     WH_HIP(hipHostMalloc((void **)&s.mega_state, sizeof(int32_t) * 8, hipHostMallocDefault));
     WH_HIP(hipStreamSynchronize(s.st));
@@ -404,9 +404,8 @@ int mega_run(wh_seq &s, int n, float inv_temp, int suppress_nst, float nst, int 
     WH_HIP(hipMemcpyAsync(s.mega_state + 4, a.err, sizeof(unsigned), hipMemcpyDeviceToHost, s.st));
     WH_HIP(hipStreamSynchronize(s.st));
     if (s.mega_state[4] != 0) {
-        // a bounded wait expired: reset the exchange state and disable the path
+        // a bounded wait expired: disable the path for this sequence
         s.mega_ok = false;
-        (void)hipMemsetAsync(a.flags, 0, sizeof(unsigned) * s.mega_grid * mega::FLAG_STRIDE, s.st);
         (void)hipMemsetAsync(a.err, 0, sizeof(unsigned), s.st);
         (void)hipStreamSynchronize(s.st);
         return fail(WH_ERR_HIP, "persistent decode: a workgroup wait timed out");
