@@ -457,7 +457,7 @@ __device__ __forceinline__ void opaque_slot(uint4 &a, uint4 &b, uint32_t &s, uin
 // row r0 + cw + NC*k (cw = cwave()) with the padded LDS vector xs of nb
 // blocks. Lanes past the last block and rows past r1 compute on duplicate
 // data and add zero; the communication wave returns zeros.
-template <int TYPE, int MAXS, int PASSES>
+template <int TYPE, int MAXS, int PASSES, int NK = MAXS / PASSES>
 __device__ __forceinline__ void row_dots(const Pre<TYPE, MAXS> &P, int nb, int r0, int r1, const float *xs,
                                          float (&out)[MAXS / PASSES]) {
     const int lane = tid() & 63, cw = cwave();
@@ -471,7 +471,7 @@ __device__ __forceinline__ void row_dots(const Pre<TYPE, MAXS> &P, int nb, int r
         float xr[32];
         lds_block(xs, min(b, nb - 1), xr);
 #pragma unroll
-        for (int k = 0; k < K; k++) {
+        for (int k = 0; k < NK; k++) {  // rows past NK per wave are known empty
             const int s = k * PASSES + p;
             const int r = r0 + cw + NC * k;
             uint4 qa = P.a[s], qb = P.b[s];
@@ -482,7 +482,7 @@ __device__ __forceinline__ void row_dots(const Pre<TYPE, MAXS> &P, int nb, int r
         }
     }
 #pragma unroll
-    for (int k = 0; k < K; k++) out[k] = wave_sum(out[k]);
+    for (int k = 0; k < NK; k++) out[k] = wave_sum(out[k]);
 }
 
 // out[lane] for lane < K (the row a lane finishes in an epilogue). out[] is
@@ -562,14 +562,21 @@ __device__ __forceinline__ void logits_chunk(const MegaArgs &a, const Pre<TYPE, 
 __host__ __device__ inline int layer_floats(int L) { return (int)((L * sizeof(MegaLayer) + 15) / 16 * 4); }
 __host__ __device__ inline int pen_floats(int V, int W) { return ((V + W - 1) / W + 3) / 4 * 4; }
 
-// Rows of phase B1 of one layer, loaded by the compute waves a phase ahead.
-// Item workgroups: their share of the head's cross-query rows in pq's first
-// SCQ slots and the query bias. Side workgroups (decoder.go:780-790 under the
-// reference mask): q,k,v rows and the v bias, and the next layer's
-// self-attention output rows with their bias and that layer's V0 (3 elements
-// per compute thread). The communication wave loads the LN parameters.
+// Rows of phase B1 of one layer. Item workgroups load their share of the
+// head's cross-query rows and the query bias a phase ahead (loop carried).
+// Side workgroups (decoder.go:780-790 under the reference mask) load their q,k,v
+// rows with the v bias and the next layer's self-attention output rows with
+// their bias and that layer's V0 (3 elements per compute thread) only once x_l
+// has arrived: their work has slack, and a prefetch at the end of F would
+// contend with the exchange polls for the memory pipeline. The communication
+// wave loads the LN parameters.
 template <int TYPE>
-struct B1Pre {
+struct B1Item {
+    Pre<TYPE, SCQ> pc;
+    float qb;
+};
+template <int TYPE>
+struct B1Side {
     Pre<TYPE, SQ> pq;
     Pre<TYPE, SO> po;
     float qb, ob;
@@ -595,19 +602,20 @@ __device__ __forceinline__ void v0_store(const float (&v0r)[3], float *v0, int d
         if (c + NCT * j < d) v0[pad(c + NCT * j)] = v0r[j];
 }
 
+// Item rows of B1 (zeros for side workgroups).
 template <int TYPE>
-__device__ __forceinline__ void b1_prefetch(B1Pre<TYPE> &S, const MegaArgs &a, const MegaLayer *ls, int l, bool item,
-                                            int cq0, int cq1, int q0, int q1, int o0, int o1, int nbd) {
+__device__ __forceinline__ void b1_item_prefetch(B1Item<TYPE> &S, const MegaLayer *ls, int l, bool item, int cq0,
+                                                 int cq1, int nbd) {
     const MegaLayer &Ly = ls[l];
-    if (item) {
-        S.qb = lane_bias<SQ>(glob<gf>(Ly.cqb), cq0, cq1);
-        prefetch<TYPE, SQ, 1, SCQ>(S.pq, uview(Ly.cq), nbd, cq0, cq1);
-        prefetch<TYPE, SO, 1, 0>(S.po, uview(Ly.so), nbd, 0, 0);
-        S.ob = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 3; j++) S.v0r[j] = 0.0f;
-        return;
-    }
+    S.qb = item ? lane_bias<SCQ>(glob<gf>(Ly.cqb), cq0, cq1) : 0.0f;
+    if (item) prefetch<TYPE, SCQ, 1>(S.pc, uview(Ly.cq), nbd, cq0, cq1);
+    else prefetch<TYPE, SCQ, 1, 0>(S.pc, uview(Ly.cq), nbd, 0, 0);
+}
+
+template <int TYPE>
+__device__ __forceinline__ void b1_side_load(B1Side<TYPE> &S, const MegaArgs &a, const MegaLayer *ls, int l, int q0,
+                                             int q1, int o0, int o1, int nbd) {
+    const MegaLayer &Ly = ls[l];
     {
         // v rows take the v bias; k rows have none; q rows are not used
         const int lane = tid() & 63, cw = max(cwave(), 0);
@@ -618,7 +626,6 @@ __device__ __forceinline__ void b1_prefetch(B1Pre<TYPE> &S, const MegaArgs &a, c
     const MegaLayer &Ln = ls[min(l + 1, a.L - 1)];
     S.ob = lane_bias<SO>(glob<gf>(Ln.sob), o0, o1);
     v0_load<TYPE>(S.v0r, a, Ln);
-    // the rows last: the first wait for the LN parameters then leaves them in flight
     prefetch<TYPE, SQ, 1>(S.pq, uview(Ly.sqkv), nbd, q0, q1);
     prefetch<TYPE, SO, 1>(S.po, uview(Ln.so), nbd, o0, o1);
 }
@@ -638,6 +645,21 @@ __device__ __forceinline__ void stage_k(const float *crossK, int enc_len, int ih
         if (v < nvec)
             __builtin_amdgcn_global_load_lds((void __attribute__((address_space(1))) *)(src + 4 * v),
                                              (void __attribute__((address_space(3))) *)(kst + b * 256), 16, 0, 0);
+    }
+}
+
+// Rows [t0, t1) of head ih of a [enc_len][64] block (cross K or V of one
+// layer) into registers of the compute waves: compute thread c holds elements
+// 4(c & 15) .. +3 of keys t0 + 28 j + (c >> 4), j < PVK. Keys past the chunk
+// re-read its last key; the communication wave holds zeros.
+__device__ __forceinline__ void chunk_rows(float4 (&r)[PVK], const float *base, int enc_len, int ih, int t0, int t1) {
+    gf *src = glob<gf>(base) + ((size_t)ih * enc_len + t0) * 64;
+    const unsigned c = (unsigned)ctid(), n = (unsigned)(t1 - t0);
+    const bool cwv = cwave() >= 0;
+#pragma unroll
+    for (int j = 0; j < PVK; j++) {
+        const unsigned t = min((unsigned)j * (NCT / 16) + (c >> 4), n - 1u);
+        r[j] = cwv ? ld16f(src + t * 64u + 4u * (c & 15u)) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 }
 
@@ -697,12 +719,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
     // self-attention output rows and V0) and the B1 rows of layer 0.
     Pre<TYPE, SO> pS;
     float obS, v0S[3];
-    B1Pre<TYPE> nb1;
+    B1Item<TYPE> nb1;
     v0_load<TYPE>(v0S, a, ls[0]);
     obS = lane_bias<SO>(glob<gf>(ls[0].sob), o0, o1);
     prefetch<TYPE, SO, 1>(pS, uview(ls[0].so), nbd, o0, o1);
     if (has_item) stage_k(ls[0].crossK, a.enc_len, ih, t0, t1, kst);
-    b1_prefetch<TYPE>(nb1, a, ls, 0, has_item, cq0, cq1, q0, q1, o0, o1, nbd);
+    b1_item_prefetch<TYPE>(nb1, ls, 0, has_item, cq0, cq1, nbd);
 
     for (int step = 0; step < a.n_steps; step++) {
         const int pos = len - 1;
@@ -729,7 +751,6 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
             // layer 0: sa_0 carries phase gin (x_0 is local); later layers: x_l carries gin
             const unsigned gin = g;
             const MegaLayer &Ly = ls[l];
-            float4 vr[PVK];          // V rows of this item's chunk (C), loaded after B1's dots
             Pre<TYPE, SD> pd;        // D's rows, loaded after C (items) or B1 (side)
             float cb;
             // ---------------- B1: cross q rows (items) / side rows ----------------
@@ -755,62 +776,53 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                     ln_wave<XD>(x, d, lp, xn);
                 }
                 TRACE(step, l, 1, 1);
-            } else if (!has_item) {
-                v0_store(nb1.v0r, v0, d);
             }
             __syncthreads();
             ++g;
             const unsigned gB1 = g;  // items' cross-query rows; side workgroups' sa_{l+1} rows
+            float4 vr[PVK];  // V rows of this item's chunk for C (zeros elsewhere)
             if (has_item) {
                 {
-                    float out[SQ];
-                    row_dots<TYPE, SQ, 1>(nb1.pq, nbd, cq0, cq1, xn, out);
-                    post<SQ>(obi, obv, lane_row<SQ>(cq0, cq1), pick<SQ>(out) + nb1.qb);
+                    float out[SCQ];
+                    row_dots<TYPE, SCQ, 1>(nb1.pc, nbd, cq0, cq1, xn, out);
+                    post<SCQ>(obi, obv, lane_row<SCQ>(cq0, cq1), pick<SCQ>(out) + nb1.qb);
                 }
                 __syncthreads();
                 TRACE(step, l, 1, 2);
-                if (comm()) flush<SQ>(obi, obv, a.qx, gB1);
-                {
-                    // C's V rows (zeros in the communication wave)
-                    gf *Vv = glob<gf>(Ly.crossV) + (size_t)ih * a.enc_len * 64;
-                    const int c = ctid();
-                    const bool cwv = cwave() >= 0;
-#pragma unroll
-                    for (int j = 0; j < PVK; j++) {
-                        const int t = min(t0 + (j * NCT + c) / 16, t1 - 1);
-                        vr[j] = cwv ? ld16f(Vv + (unsigned)t * 64u + 4u * (unsigned)(c & 15))
-                                    : make_float4(0.f, 0.f, 0.f, 0.f);
-                    }
-                }
+                if (comm()) flush<SCQ>(obi, obv, a.qx, gB1);
                 prefetch<TYPE, SD, 1, 0>(pd, uview(Ly.co), nbd, 0, 0);  // zeros until C
                 cb = 0.0f;
             } else {
+#pragma unroll
+                for (int j = 0; j < PVK; j++) vr[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                B1Side<TYPE> sp;
+                b1_side_load<TYPE>(sp, a, ls, l, q0, q1, o0, o1, nbd);
+                v0_store(sp.v0r, v0, d);
+                __syncthreads();
                 {
                     float out[SQ];
-                    row_dots<TYPE, SQ, 1>(nb1.pq, nbd, q0, q1, xn, out);
+                    row_dots<TYPE, SQ, 1>(sp.pq, nbd, q0, q1, xn, out);
                     const float v = pick<SQ>(out);
                     const int r = lane_row<SQ>(q0, q1);
                     // rows [0,d) q (unused under the reference mask), [d,2d) k, [2d,3d) v; the
                     // cache rows are read only after the launch, so the compute lanes store them
                     if (r >= d) {
                         const int j = r % d, hh = j / 64, cidx = j % 64;
-                        const bool isv = r >= 2 * d;  // nb1.qb holds this lane's v bias then
+                        const bool isv = r >= 2 * d;  // sp.qb holds this lane's v bias then
                         gfw *kv = glob<gfw>(Ly.kv);
                         kv[(isv ? (size_t)H * a.ctx * 64 : 0) + (size_t)hh * a.ctx * 64 + (size_t)pos * 64 + cidx] =
-                            isv ? v + nb1.qb : v;
+                            isv ? v + sp.qb : v;
                     }
                 }
                 {
                     float out[SO];
-                    row_dots<TYPE, SO, 1>(nb1.po, nbd, o0, o1, v0, out);
-                    post<SO>(obi, obv, l + 1 < L ? lane_row<SO>(o0, o1) : -1, pick<SO>(out) + nb1.ob);
+                    row_dots<TYPE, SO, 1>(sp.po, nbd, o0, o1, v0, out);
+                    post<SO>(obi, obv, l + 1 < L ? lane_row<SO>(o0, o1) : -1, pick<SO>(out) + sp.ob);
                 }
                 __syncthreads();
                 TRACE(step, l, 1, 2);
                 // sa_{l+1}, read in F of this layer
                 if (comm()) flush<SO>(obi, obv, a.sa + (size_t)((l + 1) & 1) * d, gB1);
-#pragma unroll
-                for (int j = 0; j < PVK; j++) vr[j] = make_float4(0.f, 0.f, 0.f, 0.f);
                 // D's rows (B2 and C are item work)
                 prefetch<TYPE, SD, 1>(pd, uview(Ly.co), nbd, rd0, rd1);
                 cb = lane_bias<SD>(glob<gf>(Ly.cob), rd0, rd1);
@@ -826,24 +838,32 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                     TRACE(step, l, 0, 1);
                 }
                 __syncthreads();
-                const float4 q4 = ((const float4 *)qh)[tid() & 15];
-                const float4 *k4 = (const float4 *)kst;
-                float mx = -INFINITY;
+                TRACEC(step, l, 0, 3);
+                // 16 lanes per key, 4 elements each; key k of the chunk is 32 j + (thread >> 4).
+                // Keys past the chunk re-read its last key: they rewrite that key's score and
+                // add nothing new to the maximum.
+                {
+                    const int tt = tid();
+                    const int n = t1 - t0, kb = tt >> 4, e4 = tt & 15;
+                    const float4 q4 = ((const float4 *)qh)[e4];
+                    const float4 *k4 = (const float4 *)kst;
+                    float part[PKV];
 #pragma unroll
-                for (int j = 0; j < PKV; j++) {
-                    const int tu = t0 + (j * NT + tid()) / 16;
-                    // keys past the chunk re-read its last staged key; the scores drop them
-                    const int t = min(tu, t1 - 1);
-                    const float4 kr = k4[(t - t0) * 16 + (tid() & 15)];
-                    const float part = row_sum16(q4.x * kr.x + q4.y * kr.y + q4.z * kr.z + q4.w * kr.w);
-                    if (tu < t1) {
-                        const float s = part * a.scale;
-                        if ((tid() & 15) == 0) sc[tu - t0] = s;
-                        mx = fmaxf(mx, s);
+                    for (int j = 0; j < PKV; j++) {
+                        const float4 kr = k4[min(kb + 32 * j, n - 1) * 16 + e4];
+                        part[j] = q4.x * kr.x + q4.y * kr.y + q4.z * kr.z + q4.w * kr.w;
                     }
+                    float mx = -INFINITY;
+#pragma unroll
+                    for (int j = 0; j < PKV; j++) {
+                        const float sj = row_sum16(part[j]) * a.scale;
+                        if (e4 == 0) sc[min(kb + 32 * j, n - 1)] = sj;
+                        mx = fmaxf(mx, sj);
+                    }
+                    mx = wave_max(mx);
+                    if (lane == 0) red[wave] = mx;
                 }
-                mx = wave_max(mx);
-                if (lane == 0) red[wave] = mx;
+                TRACEC(step, l, 0, 4);
                 __syncthreads();
                 TRACE(step, l, 0, 2);
                 if (comm() && tid() == 0) {
@@ -851,6 +871,10 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                     for (int i = 1; i < NW; i++) m = fmaxf(m, red[i]);
                     st_pair(&a.cmax[item], m, gB);
                 }
+                // C's V rows, issued after the barrier: issuing 70 KiB of loads keeps the
+                // compute waves busy for a while
+                chunk_rows(vr, Ly.crossV, a.enc_len, ih, t0, t1);
+                TRACEC(step, l, 0, 5);
             }
             // ---------------- C: softmax weights, partial P.V, head combine ----------------
             ++g;
@@ -867,19 +891,28 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                     if (lane == 0) red[32] = M;
                 }
                 __syncthreads();
-                if (cw >= 0) {
+                {
+                    // fast-exp weight of each key once (internal/ml/attention.go:34-131), in place of its score
                     const float M = red[32];
-                    const int c = ctid();
-                    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
                     float es = 0.0f;
+                    for (int t = tid(); t < t1 - t0; t += NT) {
+                        const float e = fast_exp(sc[t] - M);
+                        sc[t] = e;
+                        es += e;
+                    }
+                    es = wave_sum(es);
+                    if ((tid() & 63) == 0) red[48 + (tid() >> 6)] = es;
+                }
+                __syncthreads();
+                if (cw >= 0) {
+                    const unsigned c = (unsigned)ctid(), n = (unsigned)(t1 - t0);
+                    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
                     for (int j = 0; j < PVK; j++) {
-                        const int t = t0 + (j * NCT + c) / 16;
-                        if (t < t1) {
-                            const float e = fast_exp(sc[t - t0] - M);
-                            acc.x += e * vr[j].x; acc.y += e * vr[j].y; acc.z += e * vr[j].z; acc.w += e * vr[j].w;
-                            if ((c & 15) == 0) es += e;
-                        }
+                        // keys past the chunk (their V rows re-read the last key) add zero
+                        const unsigned t = (unsigned)j * (NCT / 16) + (c >> 4);
+                        const float e = t < n ? sc[min(t, n - 1u)] : 0.0f;
+                        acc.x += e * vr[j].x; acc.y += e * vr[j].y; acc.z += e * vr[j].z; acc.w += e * vr[j].w;
                     }
 #pragma unroll
                     for (int o = 16; o < 64; o <<= 1) {
@@ -888,10 +921,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                         acc.z += __shfl_xor(acc.z, o, 64);
                         acc.w += __shfl_xor(acc.w, o, 64);
                     }
-                    es = wave_sum(es);
                     float4 *red4 = (float4 *)xn;  // [NC][16]
                     if (lane < 16) red4[cw * 16 + lane] = acc;
-                    if (lane == 0) red[cw] = es;
                 }
                 __syncthreads();
                 if (cw >= 0) {
@@ -914,7 +945,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                     }
                     if (lane == 0) {
                         float s = 0.0f;
-                        for (int v2 = 0; v2 < NC; v2++) s += red[v2];
+                        for (int v2 = 0; v2 < NW; v2++) s += red[48 + v2];
                         st_pair(&pv[64], s, gC);
                     }
                     if (ic == 0) {
@@ -1026,9 +1057,9 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 if (comm()) flush<SD>(obi, obv, a.xg, g);
                 TRACE(step, l, 5, 6);
                 if (l + 1 < L) {
-                    // the next layer's K chunk (this layer's was consumed in B2), then its B1 rows
+                    // the next layer's K rows (this layer's were consumed in B2), then its B1 rows
                     if (has_item) stage_k(ls[l + 1].crossK, a.enc_len, ih, t0, t1, kst);
-                    b1_prefetch<TYPE>(nb1, a, ls, l + 1, has_item, cq0, cq1, q0, q1, o0, o1, nbd);
+                    b1_item_prefetch<TYPE>(nb1, ls, l + 1, has_item, cq0, cq1, nbd);
                 }
             }
         }
@@ -1121,13 +1152,13 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 }
                 if (tid() == 0) red[63] = __int_as_float(id);
             }
-            // the next step's S and B1 rows and its first K chunk (the communication
-            // wave, done with its part, fills zeros)
+            // the next step's S and B1 rows and its first K rows (the communication wave, done
+            // with its part, fills zeros)
             v0_load<TYPE>(v0S, a, ls[0]);
             obS = lane_bias<SO>(glob<gf>(ls[0].sob), o0, o1);
             prefetch<TYPE, SO, 1>(pS, uview(ls[0].so), nbd, o0, o1);
             if (has_item) stage_k(ls[0].crossK, a.enc_len, ih, t0, t1, kst);
-            b1_prefetch<TYPE>(nb1, a, ls, 0, has_item, cq0, cq1, q0, q1, o0, o1, nbd);
+            b1_item_prefetch<TYPE>(nb1, ls, 0, has_item, cq0, cq1, nbd);
             g = gT;
             __syncthreads();
             tok = __float_as_int(red[63]);
