@@ -272,29 +272,44 @@ __device__ __forceinline__ void ln_params(LnW<K> &p, gf *w, gf *b, int n) {
     }
 }
 
+// Sum of v[0..K) as a balanced binary tree (a fixed order, short dependency
+// chains).
+template <int K>
+__device__ __forceinline__ float tree_sum(const float (&v)[K]) {
+    float t[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) t[k] = v[k];
+#pragma unroll
+    for (int w = 1; w < K; w *= 2) {
+#pragma unroll
+        for (int k = 0; k + w < K; k += 2 * w) t[k] += t[k + w];
+    }
+    return t[0];
+}
+
 // LayerNorm (internal/ml/ops.go:153-202) by one wave of the n values
 // x[k] = element lane + 64k, into padded LDS xo: the mean, then the mean of
-// squared deviations, sqrt in float64, each element w * (x - mean) / sd + b.
-// No barrier: the sums are wave reductions.
+// squared deviations, sqrt in float64, each element w * (x - mean) * (1/sd) + b
+// (one reciprocal instead of a division per element: they differ by at most
+// an ulp). No barrier: the sums are wave reductions.
 template <int K>
 __device__ __forceinline__ void ln_wave(const float (&x)[K], int n, const LnW<K> &p, float *xo) {
     const int lane = tid() & 63;
-    float s = 0.0f;
+    float t[K];
 #pragma unroll
-    for (int k = 0; k < K; k++) s += (lane + 64 * k < n) ? x[k] : 0.0f;
-    const float mean = wave_sum(s) / (float)n;
-    float q = 0.0f;
+    for (int k = 0; k < K; k++) t[k] = (lane + 64 * k < n) ? x[k] : 0.0f;
+    const float mean = wave_sum(tree_sum<K>(t)) / (float)n;
 #pragma unroll
     for (int k = 0; k < K; k++) {
         const float u = x[k] - mean;
-        q += (lane + 64 * k < n) ? u * u : 0.0f;
+        t[k] = (lane + 64 * k < n) ? u * u : 0.0f;
     }
-    const float var = wave_sum(q) / (float)n;
-    const float sd = (float)sqrt((double)(var + 1e-5f));
+    const float var = wave_sum(tree_sum<K>(t)) / (float)n;
+    const float rsd = 1.0f / (float)sqrt((double)(var + 1e-5f));
 #pragma unroll
     for (int k = 0; k < K; k++) {
         const int i = lane + 64 * k;
-        if (i < n) xo[pad(i)] = p.w[k] * (x[k] - mean) / sd + p.b[k];
+        if (i < n) xo[pad(i)] = p.w[k] * (x[k] - mean) * rsd + p.b[k];
     }
 }
 
