@@ -589,11 +589,115 @@ int launch_cross_attn(const float *q, const float *const *kbase, const float *co
 // ---------------------------------------------------------------------------
 // Cross K/V projection: C[t, r] = sum_c E[t, c] * W[r, c] (+ bias[r]) for all
 // encoder frames (internal/model/decoder.go:923-940 via
-// internal/ml/matmul_q8.go:141-196). Tiled fp32 GEMM: a 64x64 output tile per
-// block, K-steps of one 32-weight block dequantised bit-exactly into LDS.
+// internal/ml/matmul_q8.go:141-196), on the fp32 matrix cores. A 64 (frames) x
+// 64 (rows) output tile per workgroup of 4 waves, each wave a 32x32 quarter
+// accumulated by v_mfma_f32_32x32x2_f32; K-steps of one 32-weight block: the
+// E tile and the weight tile (dequantised bit-exactly, 8 weights per thread)
+// go through LDS.
 // ---------------------------------------------------------------------------
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Weights 8g .. 8g+7 of block b of row r, dequantised exactly as dequant_elem.
+template <int TYPE>
+__device__ __forceinline__ void dequant8(const MatView &m, int r, int b, int g, float (&o)[8]) {
+#pragma clang fp contract(off)
+    const size_t blk = (size_t)r * m.nb + b;
+    if constexpr (TYPE == 0) {
+        const float4 *p = (const float4 *)((const float *)m.qs + blk * 32 + 8 * g);
+        const float4 x = p[0], y = p[1];
+        o[0] = x.x; o[1] = x.y; o[2] = x.z; o[3] = x.w; o[4] = y.x; o[5] = y.y; o[6] = y.z; o[7] = y.w;
+    } else if constexpr (TYPE == 8) {
+        const float d = h2f(((const uint16_t *)m.sc)[blk]);
+        const uint2 q = *(const uint2 *)(m.qs + blk * 32 + 8 * g);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t w = j < 4 ? q.x : q.y;
+            o[j] = d * (float)(int)(int8_t)(w >> (8 * (j & 3)));
+        }
+    } else {
+        const uint32_t bytes = *(const uint32_t *)(m.qs + blk * 16 + 4 * g);  // weights 8g .. 8g+7
+        uint32_t hb = 0;
+        if constexpr (TYPE == 6 || TYPE == 7) hb = (m.qh[blk] >> (8 * g)) & 0xFFu;
+        float d, mn = 0.0f;
+        if constexpr (TYPE == 3 || TYPE == 7) {
+            const uint32_t w = ((const uint32_t *)m.sc)[blk];
+            d = h2f(w & 0xFFFFu);
+            mn = h2f(w >> 16);
+        } else {
+            d = h2f(((const uint16_t *)m.sc)[blk]);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t byte = (bytes >> (8 * (j >> 1))) & 0xFFu;
+            uint32_t nib = (j & 1) ? (byte >> 4) : (byte & 0xFu);
+            if constexpr (TYPE == 6 || TYPE == 7) nib |= ((hb >> j) & 1u) << 4;
+            if constexpr (TYPE == 2) o[j] = d * (float)((int32_t)nib - 8);
+            else if constexpr (TYPE == 3) o[j] = mul_add_nofma(d, (float)nib, mn);
+            else if constexpr (TYPE == 6) o[j] = d * (float)((int32_t)nib - 16);
+            else o[j] = mul_add_nofma(d, (float)nib, mn);
+        }
+    }
+}
+
 template <int TYPE>
 __global__ __launch_bounds__(256) void k_cross_gemm(MatView w, const float *E, int T, const float *bias, float *C) {
+    __shared__ float Es[64][33];  // [frame][k]; the padding keeps the operand reads conflict-free
+    __shared__ float Ws[64][33];  // [row][k]
+    const int t0 = blockIdx.y * 64, r0 = blockIdx.x * 64;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wt = (wave >> 1) * 32, wr = (wave & 1) * 32;  // this wave's quarter of the tile
+    const int K = w.cols;
+    const int lr = tid >> 2, lg = tid & 3;  // tile loads: row (frame) lr, elements 8 lg .. 8 lg + 7
+    f32x16 acc = {};
+    for (int b = 0; b < w.nb; b++) {
+        {
+            const int t = t0 + lr;
+            float4 x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
+            if (t < T) {
+                const float4 *p = (const float4 *)(E + (size_t)t * K + b * 32 + 8 * lg);
+                x = p[0];
+                y = p[1];
+            }
+            float *e = &Es[lr][8 * lg];
+            e[0] = x.x; e[1] = x.y; e[2] = x.z; e[3] = x.w; e[4] = y.x; e[5] = y.y; e[6] = y.z; e[7] = y.w;
+        }
+        {
+            const int r = r0 + lr;
+            float o[8];
+            if (r < w.rows) {
+                dequant8<TYPE>(w, r, b, lg, o);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; j++) o[j] = 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) Ws[lr][8 * lg + j] = o[j];
+        }
+        __syncthreads();
+        // A (32 frames x 2 k): lane -> frame lane % 32, k lane / 32; B (2 k x 32 rows) likewise
+#pragma unroll
+        for (int kk = 0; kk < 32; kk += 2) {
+            const float av = Es[wt + (lane & 31)][kk + (lane >> 5)];
+            const float bv = Ws[wr + (lane & 31)][kk + (lane >> 5)];
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
+        }
+        __syncthreads();
+    }
+    // D (32 x 32): lane l, register i -> frame 8 (i / 4) + 4 (l / 32) + i % 4, row l % 32
+    const int r = r0 + wr + (lane & 31);
+    const float bb = (bias && r < w.rows) ? bias[r] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int t = t0 + wt + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        if (t < T && r < w.rows) C[(size_t)t * w.rows + r] = bias ? acc[i] + bb : acc[i];
+    }
+}
+
+// The same product on the vector units for a row length that is not a whole
+// number of blocks (small test models): one 32-column block per K-step,
+// element-wise dequantisation, columns past the row end read as zero.
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_cross_gemm_simt(MatView w, const float *E, int T, const float *bias, float *C) {
     __shared__ float Es[32][64 + 4];
     __shared__ float Ws[32][64 + 4];
     const int t0 = blockIdx.y * 64, r0 = blockIdx.x * 64;
@@ -643,6 +747,20 @@ __global__ __launch_bounds__(256) void k_cross_gemm(MatView w, const float *E, i
 int launch_cross_gemm(const DevMat &w, const float *enc, int enc_len, const float *bias, float *out, hipStream_t st) {
     MatView v = view_of(w);
     dim3 grid((w.rows + 63) / 64, (enc_len + 63) / 64);
+    if (w.cols % 32 != 0 || (((uintptr_t)enc) & 15) != 0) {
+        // a partial last block or unaligned frame rows: the vector-unit GEMM
+        switch (w.type) {
+        case 0: hipLaunchKernelGGL(k_cross_gemm_simt<0>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
+        case 2: hipLaunchKernelGGL(k_cross_gemm_simt<2>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
+        case 3: hipLaunchKernelGGL(k_cross_gemm_simt<3>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
+        case 6: hipLaunchKernelGGL(k_cross_gemm_simt<6>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
+        case 7: hipLaunchKernelGGL(k_cross_gemm_simt<7>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
+        case 8: hipLaunchKernelGGL(k_cross_gemm_simt<8>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
+        default: return fail(WH_ERR_UNSUPPORTED, "cross gemm: unsupported type");
+        }
+        WH_HIP(hipGetLastError());
+        return WH_OK;
+    }
     switch (w.type) {
     case 0: hipLaunchKernelGGL(k_cross_gemm<0>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
     case 2: hipLaunchKernelGGL(k_cross_gemm<2>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
