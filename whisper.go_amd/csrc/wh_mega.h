@@ -66,7 +66,7 @@ constexpr int CWAVES = WAVES - 1;  // waves 1.. hold weight rows; wave 0 polls, 
 constexpr int PKV = 9;      // scores: 32 keys per pass of 512 threads, 288 keys per chunk at most
 constexpr int PVK = 10;     // P.V: float4 of V per compute thread, 448 * 10 / 16 = 280 keys at most
 constexpr int CHUNK_MAX = 280;
-constexpr int CMIN = 4;     // key chunks per head at least (a chunk's cross-query rows fit SCQ slots)
+constexpr int CMIN = 5;     // key chunks per head at least (a chunk's cross-query rows fit SCQ slots)
 constexpr int CMAX = 8;     // key chunks per head at most (2240 encoder frames)
 constexpr int PFC2 = 3;     // fc2 input passes: n_state <= 64*3*32/4 = 1536
 constexpr int XD = 21;      // exchange pairs per lane of a d-vector load: n_state <= 1344
@@ -74,7 +74,7 @@ constexpr int XH = 12;      // exchange pairs per compute lane of the 4d-vector 
 constexpr int XP = 9;       // exchange pairs per lane of a head's chunk sums: CMAX * 65 <= 576
 constexpr int XT = 16;      // exchange pairs per lane of the argmax partials: 4 * 256
 // register slots (rows) per compute wave: a workgroup holds CWAVES * slots rows of each kind
-constexpr int SCQ = 3;      // cross query rows of one chunk: 64 / C <= 21 (C >= 4)
+constexpr int SCQ = 2;      // cross query rows of one chunk: 64 / C <= 14 (C >= 5)
 constexpr int SQ = 5;       // q,k,v side rows (also the slots the cross query rows use)
 constexpr int SO = 2;       // self-attention output side rows
 constexpr int SD = 1;       // cross output rows (also fc2 rows)
