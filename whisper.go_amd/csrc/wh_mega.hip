@@ -412,14 +412,19 @@ template <int TYPE>
 __device__ __forceinline__ float block_dot(const uint4 &a, const uint4 &b, uint32_t s, uint32_t h, const float *x) {
     float acc = 0.0f;
     if constexpr (TYPE == 8) {
+        // one convert and one fused multiply-add per weight, in two chains (even and odd words)
         const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        float acc1 = 0.0f;
 #pragma unroll
         for (int t = 0; t < 8; t++) {
             const int v = (int)w[t];
-            acc += (float)((v << 24) >> 24) * x[4 * t] + (float)((v << 16) >> 24) * x[4 * t + 1] +
-                   (float)((v << 8) >> 24) * x[4 * t + 2] + (float)(v >> 24) * x[4 * t + 3];
+            float &c = (t & 1) ? acc1 : acc;
+            c = __builtin_fmaf((float)((v << 24) >> 24), x[4 * t], c);
+            c = __builtin_fmaf((float)((v << 16) >> 24), x[4 * t + 1], c);
+            c = __builtin_fmaf((float)((v << 8) >> 24), x[4 * t + 2], c);
+            c = __builtin_fmaf((float)(v >> 24), x[4 * t + 3], c);
         }
-        return hf(s) * acc;
+        return hf(s) * (acc + acc1);
     } else {
         const uint32_t w[4] = {a.x, a.y, a.z, a.w};
         const float off = (TYPE == 2) ? 8.0f : (TYPE == 6 ? 16.0f : 0.0f);
@@ -473,7 +478,7 @@ __device__ __forceinline__ void opaque_slot(uint4 &a, uint4 &b, uint32_t &s, uin
 // blocks. Lanes past the last block and rows past r1 compute on duplicate
 // data and add zero; the communication wave returns zeros.
 template <int TYPE, int MAXS, int PASSES, int NK = MAXS / PASSES>
-__device__ __forceinline__ void row_dots(const Pre<TYPE, MAXS> &P, int nb, int r0, int r1, const float *xs,
+__device__ __forceinline__ void row_dots(Pre<TYPE, MAXS> &P, int nb, int r0, int r1, const float *xs,
                                          float (&out)[MAXS / PASSES]) {
     const int lane = tid() & 63, cw = cwave();
     constexpr int K = MAXS / PASSES;
@@ -489,10 +494,9 @@ __device__ __forceinline__ void row_dots(const Pre<TYPE, MAXS> &P, int nb, int r
         for (int k = 0; k < NK; k++) {  // rows past NK per wave are known empty
             const int s = k * PASSES + p;
             const int r = r0 + cw + NC * k;
-            uint4 qa = P.a[s], qb = P.b[s];
-            uint32_t qs = P.s[s], qh = P.h[s];
-            opaque_slot<TYPE>(qa, qb, qs, qh);
-            const float v = block_dot<TYPE>(qa, qb, qs, qh, xr);
+            // in place: the slot is dead after its dot, so no copy is made
+            opaque_slot<TYPE>(P.a[s], P.b[s], P.s[s], P.h[s]);
+            const float v = block_dot<TYPE>(P.a[s], P.b[s], P.s[s], P.h[s], xr);
             out[k] += (r < r1 && b < nb) ? v : 0.0f;
         }
     }
@@ -550,7 +554,7 @@ __device__ __forceinline__ void better(float v, int i, float &bv, int &bi) {
 // pen[r - rv0] is the window count of row r. The raw logit of the EOT row is
 // posted to LDS (*eotv) for the communication wave to publish.
 template <int TYPE>
-__device__ __forceinline__ void logits_chunk(const MegaArgs &a, const Pre<TYPE, TS> &P, int nb, int base, int end,
+__device__ __forceinline__ void logits_chunk(const MegaArgs &a, Pre<TYPE, TS> &P, int nb, int base, int end,
                                              const float *xn, const int *pen, int rv0, float &bv, int &bi,
                                              float &bv2, int &bi2, float *eotv) {
     const int lane = tid() & 63, cw = cwave();
