@@ -2,6 +2,7 @@
 // gfx950 kernel (wh_mega.hip).
 #pragma once
 
+#include <algorithm>
 #include <cstddef>
 #include <cstdint>
 
@@ -66,20 +67,43 @@ constexpr int CWAVES = WAVES - 1;  // waves 1.. hold weight rows; wave 0 polls, 
 constexpr int PKV = 9;      // scores: 32 keys per pass of 512 threads, 288 keys per chunk at most
 constexpr int PVK = 10;     // P.V: float4 of V per compute thread, 448 * 10 / 16 = 280 keys at most
 constexpr int CHUNK_MAX = 280;
-constexpr int CMIN = 5;     // key chunks per head at least (a chunk's cross-query rows fit SCQ slots)
+constexpr int CMIN = 5;     // key chunks per head at least
 constexpr int CMAX = 8;     // key chunks per head at most (2240 encoder frames)
-constexpr int PFC2 = 3;     // fc2 input passes: n_state <= 64*3*32/4 = 1536
 constexpr int XD = 21;      // exchange pairs per lane of a d-vector load: n_state <= 1344
 constexpr int XH = 12;      // exchange pairs per compute lane of the 4d-vector load: 4d <= 7*64*12
+constexpr int XS = 3;       // exchange pairs per compute lane of a d-vector load: d <= 7*64*3
 constexpr int XP = 9;       // exchange pairs per lane of a head's chunk sums: CMAX * 65 <= 576
 constexpr int XT = 16;      // exchange pairs per lane of the argmax partials: 4 * 256
 // register slots (rows) per compute wave: a workgroup holds CWAVES * slots rows of each kind
-constexpr int SCQ = 2;      // cross query rows of one chunk: 64 / C <= 14 (C >= 5)
-constexpr int SQ = 5;       // q,k,v side rows (also the slots the cross query rows use)
+constexpr int SQ = 5;       // q,k,v side rows
 constexpr int SO = 2;       // self-attention output side rows
-constexpr int SD = 1;       // cross output rows (also fc2 rows)
-constexpr int SE = 3;       // fc1 rows
+constexpr int SD = 1;       // cross output rows
 constexpr int TS = 6;       // logits rows per chunk
+// flat splits (blocks per compute lane, rows per compute wave): cross query rows
+// of a chunk, fc1 rows, fc2 rows of a workgroup
+constexpr int FQ = 1, RQ = 3;
+constexpr int FE = 2, RE = 4;
+constexpr int FF = 2, RF = 2;
+
+// Whether the flat split of nrows rows of nb blocks over the compute waves fits
+// P blocks per lane, RS rows per wave and three waves per row (the kernel's
+// limits; rows are posted by communication lanes, so nrows <= 64).
+inline bool flat_fits(int nrows, int nb, int P, int RS) {
+    if (nrows < 0 || nrows > 64 || nb <= 0 || nb > 255) return false;
+    const int n = nrows * nb;
+    int cover[64] = {0};
+    const int A = std::min(CWAVES, std::max(1, 2 * nrows));  // waves with items
+    for (int c = 0; c < A; c++) {
+        const int i0 = c * n / A, i1 = (c + 1) * n / A;
+        if (i1 - i0 > 64 * P) return false;
+        if (i1 <= i0) continue;
+        const int ra = i0 / nb, rb = (i1 - 1) / nb;
+        if (rb - ra + 1 > RS) return false;
+        for (int r = ra; r <= rb; r++)
+            if (++cover[r] > 3) return false;
+    }
+    return true;
+}
 
 // Dynamic LDS bytes of the kernel for n_state d, L layers, V vocabulary rows,
 // a grid of W workgroups and chunk_len keys per chunk.

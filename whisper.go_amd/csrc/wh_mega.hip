@@ -256,6 +256,60 @@ __device__ __forceinline__ void ll_load(float *dst, const uint64_t *src, int n, 
     }
 }
 
+// ll_load of two vectors in one wait: src1 (n1 pairs of phase g1 from first1,
+// into dst1, padded when PAD1) and src2 (n2 pairs of phase g2 from first2, into
+// plain dst2). Both are loaded up front, so a vector that is already there costs
+// no round trip of its own.
+template <int K1, bool PAD1, int K2>
+__device__ __forceinline__ void ll_load2(float *dst1, const uint64_t *src1, int n1, unsigned g1, int first1,
+                                         float *dst2, const uint64_t *src2, int n2, unsigned g2, int first2,
+                                         unsigned *err) {
+    typedef __attribute__((address_space(1))) const uint64_t gcu64;
+    typedef __attribute__((address_space(1))) const unsigned gcu;
+    const int l1 = first1 + (tid() & 63), l2 = first2 + (tid() & 63);
+    gcu64 *a8 = glob<gcu64>(src1), *b8 = glob<gcu64>(src2);
+    gcu *perr = glob<gcu>(err);
+    uint64_t v[K1], u[K2];
+#pragma unroll
+    for (int k = 0; k < K1; k++)
+        v[k] = __hip_atomic_load(a8 + min(l1 + 64 * k, n1 - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int k = 0; k < K2; k++)
+        u[k] = __hip_atomic_load(b8 + min(l2 + 64 * k, n2 - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned e = __hip_atomic_load(perr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (unsigned spins = 0;; spins++) {
+        bool ok = true;
+#pragma unroll
+        for (int k = 0; k < K1; k++) ok &= (l1 + 64 * k >= n1) || (unsigned)(v[k] >> 32) >= g1;
+#pragma unroll
+        for (int k = 0; k < K2; k++) ok &= (l2 + 64 * k >= n2) || (unsigned)(u[k] >> 32) >= g2;
+        if (__all(ok)) break;
+        if (e != 0 || spins > SPIN_MAX) {
+            if ((tid() & 63) == 0) atomicOr(err, 1u);
+            break;
+        }
+#pragma unroll
+        for (int k = 0; k < K1; k++)
+            if ((unsigned)(v[k] >> 32) < g1)
+                v[k] = __hip_atomic_load(a8 + min(l1 + 64 * k, n1 - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int k = 0; k < K2; k++)
+            if ((unsigned)(u[k] >> 32) < g2)
+                u[k] = __hip_atomic_load(b8 + min(l2 + 64 * k, n2 - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        e = __hip_atomic_load(perr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int k = 0; k < K1; k++) {
+        const int i = l1 + 64 * k;
+        if (i < n1) dst1[PAD1 ? pad(i) : i] = __uint_as_float((uint32_t)v[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < K2; k++) {
+        const int i = l2 + 64 * k;
+        if (i < n2) dst2[i] = __uint_as_float((uint32_t)u[k]);
+    }
+}
+
 // LayerNorm parameters of one wave's elements lane + 64k (k < K).
 template <int K>
 struct LnW {
@@ -535,6 +589,131 @@ __device__ __forceinline__ int lane_row(int r0, int r1) {
     return (cw >= 0 && lane < K && r < r1) ? r : -1;
 }
 
+// ---- flat split of a workgroup's rows ---------------------------------------------
+// The (row, block) items of rows [r0, r0 + nrows), nb blocks each, in row-major
+// order: item i is block r0*nb + i of the matrix, whose rows are contiguous.
+// Compute wave c < A takes items [c*N/A, (c+1)*N/A) (N = nrows*nb, A =
+// min(NC, 2 nrows) waves, so a wave holds at least half a row) and its lane l
+// the items i0 + l + 64p, p < P: every compute wave gets the same number of
+// blocks whatever the row count (a row per wave leaves lanes idle when nb is not
+// a multiple of 64 and loads some SIMDs twice as much as others), and a wave's
+// loads are consecutive blocks. A wave sums its items by row (at most RS rows,
+// counted from the row of its first item); a row can straddle two or three
+// waves, and the communication wave adds its wave sums in wave order.
+__device__ __forceinline__ int flat_i0(int c, int nrows, int nb) {
+    const int A = min(NC, max(1, 2 * nrows)), n = nrows * nb;
+    return c >= A ? n : c * n / A;
+}
+
+// Per-launch constants of a flat split for this lane. Compute lanes: pass p's
+// block within its row (bits 12p..12p+7) and wave-relative row (bits
+// 12p+8..12p+11; 15 marks a lane past the wave's items), p < 2. Communication
+// lanes t < nrows: the outbox slots of row t's wave sums in wave order (bits
+// 0-7, 8-15, 16-23) and their count (bits 24-25). The host checks the limits
+// (nb <= 255, at most 64P items and RS rows per wave, 3 waves per row).
+template <int P, int RS>
+__device__ __forceinline__ uint32_t flat_info(int nb, int nrows) {
+    static_assert(P <= 2 && RS <= 15 && NC * RS <= OUTBOX, "flat split limits");
+    const int lane = tid() & 63, cw = cwave();
+    const int n = nrows * nb;
+    uint32_t r = 0;
+    if (n <= 0) return cw >= 0 ? 0xF00F00u : 0u;
+    if (cw >= 0) {
+        const int i0 = flat_i0(cw, nrows, nb), i1 = flat_i0(cw + 1, nrows, nb), ra = i0 / nb;
+        for (int p = 0; p < P; p++) {
+            const int i = i0 + lane + 64 * p;
+            const int ic = min(i, max(i1 - 1, 0));
+            const int row = ic / nb;
+            const uint32_t rel = i < i1 ? (uint32_t)(row - ra) : 15u;
+            r |= ((uint32_t)(ic - row * nb) | rel << 8) << (12 * p);
+        }
+        if (P < 2) r |= 0xF00u << 12;
+    } else if (lane < nrows) {
+        uint32_t cnt = 0;
+        for (int c = 0; c < NC; c++) {
+            const int i0 = flat_i0(c, nrows, nb), i1 = flat_i0(c + 1, nrows, nb);
+            if (i1 <= i0) continue;
+            const int ra = i0 / nb, rb = (i1 - 1) / nb;
+            if (lane >= ra && lane <= rb && cnt < 3) {
+                r |= (uint32_t)(c * RS + lane - ra) << (8 * cnt);
+                cnt++;
+            }
+        }
+        r |= cnt << 24;
+    }
+    return r;
+}
+
+// Items of this compute lane into its P slots (zeros when !on and on the
+// communication wave). Past the wave's items a slot re-reads its last item
+// (a cache hit); with no items at all, block 0.
+template <int TYPE, int P>
+__device__ __forceinline__ void flat_prefetch(Pre<TYPE, P> &F, const UView &m, int nb, int r0, int nrows, bool on) {
+    const int lane = tid() & 63, cw = cwave();
+    const int n = nrows * nb, c = max(cw, 0);
+    const int i0 = flat_i0(c, nrows, nb), last = max(flat_i0(c + 1, nrows, nb) - 1, 0);
+    const unsigned base = n > 0 ? (unsigned)r0 * (unsigned)nb : 0u;
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+        if (cw < 0 || !on) {
+            F.a[p] = make_uint4(0u, 0u, 0u, 0u);
+            F.b[p] = make_uint4(0u, 0u, 0u, 0u);
+            F.s[p] = 0u;
+            F.h[p] = 0u;
+        } else {
+            load_blk<TYPE>(m, base + (unsigned)min(i0 + lane + 64 * p, last), F.a[p], F.b[p], F.s[p], F.h[p]);
+        }
+    }
+}
+
+// Wave sums by row of this compute wave's items: out[j] (same on every lane) is
+// the sum over its items of wave-relative row j. The communication wave returns zeros.
+template <int TYPE, int P, int RS>
+__device__ __forceinline__ void flat_dots(Pre<TYPE, P> &F, uint32_t info, const float *xs, float (&out)[RS]) {
+#pragma unroll
+    for (int j = 0; j < RS; j++) out[j] = 0.0f;
+    if (cwave() < 0) return;
+    float acc[RS];
+#pragma unroll
+    for (int j = 0; j < RS; j++) acc[j] = 0.0f;
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+        const uint32_t f = info >> (12 * p);
+        const uint32_t rel = (f >> 8) & 0xFu;
+        float xr[32];
+        lds_block(xs, (int)(f & 0xFFu), xr);
+        opaque_slot<TYPE>(F.a[p], F.b[p], F.s[p], F.h[p]);
+        const float v = block_dot<TYPE>(F.a[p], F.b[p], F.s[p], F.h[p], xr);
+#pragma unroll
+        for (int j = 0; j < RS; j++) acc[j] += rel == (uint32_t)j ? v : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < RS; j++) out[j] = wave_sum(acc[j]);
+}
+
+// Compute wave c posts its row sums into outbox slots c*RS + j.
+template <int RS>
+__device__ __forceinline__ void flat_post(float *obv, const float (&out)[RS]) {
+    const int lane = tid() & 63, cw = cwave();
+    const float v = pick<RS>(out);
+    if (cw >= 0 && lane < RS) obv[cw * RS + lane] = v;
+}
+
+// Communication lane t < nrows, after the barrier that follows the posts: row t's sum.
+__device__ __forceinline__ float flat_sum(const float *obv, uint32_t slots) {
+    const uint32_t n = slots >> 24;
+    float s = obv[slots & 0xFFu];
+    if (n > 1) s += obv[(slots >> 8) & 0xFFu];
+    if (n > 2) s += obv[(slots >> 16) & 0xFFu];
+    return s;
+}
+
+// Bias of row r0 + lane on the communication wave (clamped into [r0, r1)); zero elsewhere.
+__device__ __forceinline__ float comm_bias(gf *bias, int r0, int r1) {
+    const int lane = tid() & 63;
+    return (comm() && r1 > r0) ? bias[min(r0 + lane, r1 - 1)] : 0.0f;
+}
+
 // The tanh-form GELU of internal/ml/ops.go:102-122 with tanh in float32 (the
 // reference takes tanh in float64; the two differ by about one float32 ulp of
 // 1 + tanh, far inside the logits tolerance). The float64 tanh is a long
@@ -591,8 +770,8 @@ __host__ __device__ inline int pen_floats(int V, int W) { return ((V + W - 1) / 
 // wave loads the LN parameters.
 template <int TYPE>
 struct B1Item {
-    Pre<TYPE, SCQ> pc;
-    float qb;
+    Pre<TYPE, FQ> pc;
+    float qb;  // communication lanes: the bias of their row
 };
 template <int TYPE>
 struct B1Side {
@@ -626,9 +805,8 @@ template <int TYPE>
 __device__ __forceinline__ void b1_item_prefetch(B1Item<TYPE> &S, const MegaLayer *ls, int l, bool item, int cq0,
                                                  int cq1, int nbd) {
     const MegaLayer &Ly = ls[l];
-    S.qb = item ? lane_bias<SCQ>(glob<gf>(Ly.cqb), cq0, cq1) : 0.0f;
-    if (item) prefetch<TYPE, SCQ, 1>(S.pc, uview(Ly.cq), nbd, cq0, cq1);
-    else prefetch<TYPE, SCQ, 1, 0>(S.pc, uview(Ly.cq), nbd, 0, 0);
+    S.qb = item ? comm_bias(glob<gf>(Ly.cqb), cq0, cq1) : 0.0f;
+    flat_prefetch<TYPE, FQ>(S.pc, uview(Ly.cq), nbd, cq0, cq1 - cq0, item);
 }
 
 template <int TYPE>
@@ -704,6 +882,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
     float *sc = (float *)(hl + 128);      // [32*PKV] scores of this workgroup's chunk
     int *pen = (int *)(sc + 32 * PKV);    // [pen_floats] window counts of this workgroup's vocabulary rows
     float *kst = (float *)pen + pen_floats(a.V, gridDim.x);  // [chunk_len * 64] K rows of this item's chunk
+    uint32_t *fil = (uint32_t *)(kst + a.chunk_len * 64);     // [3][NT] flat-split constants by thread
     __shared__ float eotv;
     __shared__ int eotf;
 
@@ -729,6 +908,11 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
     const int rd0 = (int)((long)w * d / W), rd1 = (int)((long)(w + 1) * d / W);
     const int rf0 = (int)((long)w * 4 * d / W), rf1 = (int)((long)(w + 1) * 4 * d / W);
     const int rv0 = (int)((long)w * a.V / W), rv1 = (int)((long)(w + 1) * a.V / W);
+    // flat splits of the cross-query (items), fc1 and fc2 rows
+    // (kept in LDS: registers are short in the logits phase)
+    fil[tid()] = flat_info<FQ, RQ>(nbd, has_item ? cq1 - cq0 : 0);
+    fil[NT + tid()] = flat_info<FE, RE>(nbd, rf1 - rf0);
+    fil[2 * NT + tid()] = flat_info<FF, RF>(nbf, rd1 - rd0);
 
     unsigned g = a.g0;
     int tok = a.tok0, len = a.len0, prev = a.prev0, streak = a.streak0;
@@ -802,13 +986,16 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
             float4 vr[PVK];  // V rows of this item's chunk for C (zeros elsewhere)
             if (has_item) {
                 {
-                    float out[SCQ];
-                    row_dots<TYPE, SCQ, 1>(nb1.pc, nbd, cq0, cq1, xn, out);
-                    post<SCQ>(obi, obv, lane_row<SCQ>(cq0, cq1), pick<SCQ>(out) + nb1.qb);
+                    float out[RQ];
+                    flat_dots<TYPE, FQ, RQ>(nb1.pc, fil[tid()], xn, out);
+                    flat_post<RQ>(obv, out);
                 }
                 __syncthreads();
                 TRACE(step, l, 1, 2);
-                if (comm()) flush<SCQ>(obi, obv, a.qx, gB1);
+                if (comm()) {
+                    const int t = tid();
+                    if (t < cq1 - cq0) st_pair(&a.qx[cq0 + t], flat_sum(obv, fil[t]) + nb1.qb, gB1);
+                }
                 prefetch<TYPE, SD, 1, 0>(pd, uview(Ly.co), nbd, 0, 0);  // zeros until C
                 cb = 0.0f;
             } else {
@@ -981,7 +1168,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 }
             }
             // ---------------- D: cross out rows -> x2 ----------------
-            Pre<TYPE, SE> pe;
+            Pre<TYPE, FE> pe;
             float fbE;
             {
                 TRACE(step, l, 3, 0);
@@ -1008,12 +1195,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 ++g;
                 if (comm()) flush<SD>(obi, obv, a.x2, g);
                 // E's bias and rows
-                fbE = lane_bias<SE>(glob<gf>(Ly.fc1b), rf0, rf1);
-                prefetch<TYPE, SE, 1>(pe, uview(Ly.fc1), nbd, rf0, rf1);
+                fbE = comm_bias(glob<gf>(Ly.fc1b), rf0, rf1);
+                flat_prefetch<TYPE, FE>(pe, uview(Ly.fc1), nbd, rf0, rf1 - rf0, true);
             }
             const unsigned gD = g;
             // ---------------- E: LN3 + fc1 + GELU ----------------
-            Pre<TYPE, SD * PFC2> pf;
+            Pre<TYPE, FF> pf;
             float fbF;
             {
                 TRACE(step, l, 4, 0);
@@ -1028,52 +1215,58 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 TRACE(step, l, 4, 4);
                 TRACEC(step, l, 4, 7);
                 {
-                    float out[SE];
-                    row_dots<TYPE, SE, 1>(pe, nbd, rf0, rf1, xn, out);
+                    float out[RE];
+                    flat_dots<TYPE, FE, RE>(pe, fil[NT + tid()], xn, out);
                     TRACEC(step, l, 4, 5);
-                    const float v = pick<SE>(out);
-                    const int r = lane_row<SE>(rf0, rf1);
-                    post<SE>(obi, obv, r, r >= 0 ? gelu_f32(v + fbE) : 0.0f);
+                    flat_post<RE>(obv, out);
                 }
                 __syncthreads();
                 TRACE(step, l, 4, 2);
                 ++g;
-                if (comm()) flush<SE>(obi, obv, a.hbuf, g);
+                if (comm()) {
+                    const int t = tid();
+                    if (t < rf1 - rf0) st_pair(&a.hbuf[rf0 + t], gelu_f32(flat_sum(obv, fil[NT + t]) + fbE), g);
+                }
                 TRACE(step, l, 4, 6);
                 // F's bias and rows
-                fbF = lane_bias<SD>(glob<gf>(Ly.fc2b), rd0, rd1);
-                prefetch<TYPE, SD * PFC2, PFC2>(pf, uview(Ly.fc2), nbf, rd0, rd1);
+                fbF = comm_bias(glob<gf>(Ly.fc2b), rd0, rd1);
+                flat_prefetch<TYPE, FF>(pf, uview(Ly.fc2), nbf, rd0, rd1 - rd0, true);
             }
             const unsigned gE = g;
             // ---------------- F: fc2 rows -> x_{l+1} ----------------
             {
                 TRACE(step, l, 5, 0);
-                // h by the compute waves (12 pairs per lane), sa_{l+1} by the communication wave
-                if (comm()) {
-                    if (l + 1 < L) ll_load<XD, false>(sav, a.sa + (size_t)((l + 1) & 1) * d, d, gB1, a.err);
-                } else {
-                    ll_load<XH, true>(xn, a.hbuf, 4 * d, gE, a.err, cwave() * 64 * XH);
+                // h (12 pairs per lane) and sa_{l+1} (3 per lane; published long ago, its
+                // loads ride along) by the compute waves
+                if (!comm()) {
+                    if (l + 1 < L)
+                        ll_load2<XH, true, XS>(xn, a.hbuf, 4 * d, gE, cwave() * 64 * XH, sav,
+                                               a.sa + (size_t)((l + 1) & 1) * d, d, gB1, cwave() * 64 * XS, a.err);
+                    else
+                        ll_load<XH, true>(xn, a.hbuf, 4 * d, gE, a.err, cwave() * 64 * XH);
+                    TRACEC(step, l, 5, 4);
                 }
                 TRACE(step, l, 5, 1);
                 __syncthreads();
                 TRACE(step, l, 5, 3);
                 {
-                    float out[SD];
-                    row_dots<TYPE, SD * PFC2, PFC2>(pf, nbf, rd0, rd1, xn, out);
+                    float out[RF];
+                    flat_dots<TYPE, FF, RF>(pf, fil[2 * NT + tid()], xn, out);
                     TRACEC(step, l, 5, 5);
-                    const float v = pick<SD>(out);
-                    const int r = lane_row<SD>(rd0, rd1);
-                    float x = 0.0f;
-                    if (r >= 0) {
-                        x = x2_own[r - rd0] + (v + fbF);
-                        xl_own[r - rd0] = x;
-                    }
-                    post<SD>(obi, obv, r, x);
+                    flat_post<RF>(obv, out);
                 }
                 __syncthreads();
                 TRACE(step, l, 5, 2);
                 ++g;
-                if (comm()) flush<SD>(obi, obv, a.xg, g);
+                if (comm()) {
+                    // x_{l+1} = x2 + (fc2 + b); D of the next layer reads the own rows
+                    const int t = tid();
+                    if (t < rd1 - rd0) {
+                        const float x = x2_own[t] + (flat_sum(obv, fil[2 * NT + t]) + fbF);
+                        xl_own[t] = x;
+                        st_pair(&a.xg[rd0 + t], x, g);
+                    }
+                }
                 TRACE(step, l, 5, 6);
                 if (l + 1 < L) {
                     // the next layer's K rows (this layer's were consumed in B2), then its B1 rows
@@ -1215,7 +1408,7 @@ extern "C" int wh_mega_trace_read(void *out, size_t bytes) {
 size_t lds_bytes(int d, int L, int V, int W, int chunk_len) {
     const int d36 = ((d + 31) / 32) * 36;
     return sizeof(float) * (size_t)(layer_floats(L) + 6 * d36 + d + 64 * 4 + 2 * OUTBOX + 64 * XT + 128 +
-                                    32 * PKV + pen_floats(V, W) + chunk_len * 64);
+                                    32 * PKV + pen_floats(V, W) + chunk_len * 64 + 3 * NT);
 }
 
 int launch_decode(uint32_t type, int grid, const MegaArgs &a, hipStream_t st) {

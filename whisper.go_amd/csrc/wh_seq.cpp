@@ -261,7 +261,7 @@ int mega_setup(wh_seq &s) {
     s.mega_ok = false;
     if (s.S != 1 || !env_int("WHISPER_HIP_PERSISTENT", 1)) return WH_OK;
     const int d = m.n_state, H = m.n_head, L = m.n_layer;
-    if (d / H != 64 || d % 64 != 0 || d > 64 * 3 * 32 / 4 || !is_quant_type(m.tok.type)) return WH_OK;
+    if (d / H != 64 || d % 64 != 0 || !is_quant_type(m.tok.type)) return WH_OK;
     for (const Layer &l : m.layers) {
         if (!l.sqkv.alloc) return WH_OK;  // q, k, v not stacked (mixed types)
         const DevMat *ms[] = {&l.sqkv, &l.so, &l.cq, &l.co, &l.fc1, &l.fc2};
@@ -273,8 +273,13 @@ int mega_setup(wh_seq &s) {
     if (hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, m.device) != hipSuccess)
         return WH_OK;
     const int W = std::min(env_int("WHISPER_HIP_GRID", dev_cus), dev_cus);
-    // C >= CMIN chunks of at most CHUNK_MAX keys; the last chunk is not empty
-    const int C = std::max(mega::CMIN, (s.enc_len + mega::CHUNK_MAX - 1) / mega::CHUNK_MAX);
+    // C >= CMIN chunks of at most CHUNK_MAX keys, enough that a chunk's share of its
+    // head's 64 cross-query rows fits the flat split; the last chunk is not empty
+    const int nbd = d / 32;
+    int C = std::max(mega::CMIN, (s.enc_len + mega::CHUNK_MAX - 1) / mega::CHUNK_MAX);
+    while (C < mega::CMAX && !(mega::flat_fits(64 / C, nbd, mega::FQ, mega::RQ) &&
+                               mega::flat_fits((64 + C - 1) / C, nbd, mega::FQ, mega::RQ)))
+        C++;
     const int chunk = (s.enc_len + C - 1) / C;
     if (s.enc_len < 16 || (C - 1) * chunk >= s.enc_len || chunk > mega::CHUNK_MAX || chunk > 32 * mega::PKV)
         return WH_OK;
@@ -282,12 +287,18 @@ int mega_setup(wh_seq &s) {
     // per-workgroup row capacities of the kernel's register slots (compute waves only)
     auto per = [&](int rows, int n) { return (rows + n - 1) / n; };
     const int NC = mega::CWAVES;
-    // LayerNorm: 3 elements per compute thread; exchange loads: XD, XH, XT, XP pairs per lane
-    if (d > 3 * 64 * NC || d > 64 * mega::XD || 4 * d > 64 * NC * mega::XH || 4 * W > 64 * mega::XT ||
+    // exchange loads: XS, XD, XH, XT, XP pairs per lane
+    if (d > 64 * NC * mega::XS || d > 64 * mega::XD || 4 * d > 64 * NC * mega::XH || 4 * W > 64 * mega::XT ||
         mega::CMAX * 65 > 64 * mega::XP)
         return WH_OK;
-    if (C > mega::CMAX || W < 8 || items >= W || W > 256 || H > 256 || per(d, W) > NC * mega::SD ||
-        per(4 * d, W) > NC * mega::SE || per(64, C) > NC * mega::SCQ || mega::SCQ > mega::SQ)
+    if (C > mega::CMAX || W < 8 || items >= W || W > 256 || H > 256 || per(d, W) > NC * mega::SD)
+        return WH_OK;
+    // flat splits: both row counts a workgroup (or item) can get
+    auto flat2 = [&](int rows, int n, int nb, int P, int RS) {
+        return mega::flat_fits(rows / n, nb, P, RS) && mega::flat_fits(per(rows, n), nb, P, RS);
+    };
+    if (!flat2(64, C, nbd, mega::FQ, mega::RQ) || !flat2(4 * d, W, nbd, mega::FE, mega::RE) ||
+        !flat2(d, W, 4 * nbd, mega::FF, mega::RF))
         return WH_OK;
     if (mega::lds_bytes(d, L, m.n_vocab, W, chunk) + 64 > (size_t)lds_max) return WH_OK;
     auto fits32 = [](const DevMat &x) { return (uint64_t)x.rows * x.nb * 32 < (1ull << 32); };
