@@ -68,6 +68,11 @@ struct Layer {
     // q, k, v stacked as one [3d, d] matrix when they share a quantised type;
     // sq/sk/sv are then views into its planes (alloc == nullptr)
     DevMat sqkv;
+    // LayerNorm folded into the rows that read its output (persistent decode):
+    // W·LN(x) = rsd * (W·(w*x) - mean * (W·w)) + (W·b + bias), so per row W·w
+    // (cqc: cross query rows with ln2; f1c: fc1 rows with ln3) and W·b + bias
+    // (cqe, f1e). Null when the matrices are not quantised.
+    float *cqc = nullptr, *cqe = nullptr, *f1c = nullptr, *f1e = nullptr;
 };
 // Stack same-type matrices with equal column counts into one allocation; the
 // parts become views into it.
@@ -85,6 +90,7 @@ struct wh_model {
     float *lnw = nullptr, *lnb = nullptr;
     std::vector<wh::Layer> layers;
     void *vec_alloc = nullptr;  // one allocation for every float vector
+    void *fold_alloc = nullptr;  // the folded LayerNorm row constants of every layer
     uint64_t weight_bytes = 0;
 };
 

@@ -14,6 +14,7 @@ namespace mega {
 struct MegaLayer {
     MatView sqkv, so, cq, co, fc1, fc2;  // sqkv: q, k, v rows stacked ([3d, d])
     const float *ln1w, *ln1b, *svb, *sob, *ln2w, *ln2b, *cqb, *cob, *ln3w, *ln3b, *fc1b, *fc2b;
+    const float *cqc, *cqe, *f1c, *f1e;  // folded LN2 / LN3 row constants (see Layer)
     const float *crossK, *crossV;  // [enc_len][d] of this layer (stream 0)
     float *kv;                     // [2][H][n_ctx][64] of this layer (stream 0)
 };

@@ -385,6 +385,103 @@ __device__ __forceinline__ void ll_load_ln(float *xo, const uint64_t *src, int n
     ln_wave<K>(x, n, p, xo);
 }
 
+// ll_load_ln with the LayerNorm weight and bias read from LDS (wl, bl [n]).
+template <int K>
+__device__ __forceinline__ void ll_load_ln_lds(float *xo, const uint64_t *src, int n, unsigned g, unsigned *err,
+                                               const float *wl, const float *bl) {
+    uint64_t v[K];
+    ll_poll<K>(v, src, n, g, err);
+    const int lane = tid() & 63;
+    float x[K], t[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        x[k] = __uint_as_float((uint32_t)v[k]);
+        t[k] = (lane + 64 * k < n) ? x[k] : 0.0f;
+    }
+    const float mean = wave_sum(tree_sum<K>(t)) / (float)n;
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const float u = x[k] - mean;
+        t[k] = (lane + 64 * k < n) ? u * u : 0.0f;
+    }
+    const float var = wave_sum(tree_sum<K>(t)) / (float)n;
+    const float rsd = 1.0f / (float)sqrt((double)(var + 1e-5f));
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int i = lane + 64 * k;
+        if (i < n) xo[pad(i)] = wl[i] * (x[k] - mean) * rsd + bl[i];
+    }
+}
+
+// ---- LayerNorm folded into the rows that read it --------------------------------
+// For a row W of the next matrix, W·LN(x) = rsd*(W·(w*x) - mean*(W·w)) + W·b:
+// the communication wave stores w*x into the padded LDS vector as soon as x has
+// arrived, the compute waves start their dots on it, and the communication wave
+// computes mean and rsd while they run; the per-row constants W·w and W·b (+
+// the row bias) come from the host.
+
+// LayerNorm weights of one wave's elements lane + 64k.
+template <int K>
+__device__ __forceinline__ void ln_gain(float (&w)[K], gf *g, int n) {
+    const int lane = tid() & 63;
+#pragma unroll
+    for (int k = 0; k < K; k++) w[k] = g[min(lane + 64 * k, n - 1)];
+}
+
+// x[k] (element lane + 64k) into padded LDS xo as w[k] * x[k].
+template <int K>
+__device__ __forceinline__ void store_scaled(const float (&x)[K], const float (&w)[K], int n, float *xo) {
+    const int lane = tid() & 63;
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int i = lane + 64 * k;
+        if (i < n) xo[pad(i)] = w[k] * x[k];
+    }
+}
+
+// Communication wave: wait for the exchanged vector src (n pairs of phase g),
+// plus the plain LDS vector add when ADD, into x (kept for ln_stats), and store w*x.
+template <int K, bool ADD>
+__device__ __forceinline__ void ll_load_scaled(float (&x)[K], float *xo, const uint64_t *src, int n, unsigned g,
+                                               unsigned *err, const float (&w)[K], const float *add) {
+    uint64_t v[K];
+    ll_poll<K>(v, src, n, g, err);
+    const int lane = tid() & 63;
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        x[k] = __uint_as_float((uint32_t)v[k]);
+        if (ADD) x[k] += add[min(lane + 64 * k, n - 1)];
+    }
+    store_scaled<K>(x, w, n, xo);
+}
+
+// Mean and 1/sd of the n values x[k] = element lane + 64k in one pass: the
+// sums of x and x*x reduce side by side (half the dependent chain of the
+// two-pass form, so it stays under the dots it overlaps), var = E[x^2] - mean^2.
+// LayerNorm inputs have a spread comparable to or above their mean, so the
+// subtraction loses no significant bits.
+template <int K>
+__device__ __forceinline__ void ln_stats(const float (&x)[K], int n, float &mean, float &rsd) {
+    const int lane = tid() & 63;
+    float s[K], q[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const float v = (lane + 64 * k < n) ? x[k] : 0.0f;
+        s[k] = v;
+        q[k] = v * v;
+    }
+    const float S = wave_sum(tree_sum<K>(s)), Q = wave_sum(tree_sum<K>(q));
+    const float inv_n = 1.0f / (float)n;
+    mean = S * inv_n;
+    const float var = fmaxf(Q * inv_n - mean * mean, 0.0f);
+    rsd = 1.0f / (float)sqrt((double)(var + 1e-5f));
+}
+
+// A folded row's value from its dot with w*x.
+__device__ __forceinline__ float ln_fold(float dot, float mean, float rsd, float c, float e) {
+    return rsd * (dot - mean * c) + e;
+}
+
 // ---- outbox: compute lanes post (row, value); the communication wave stores ----
 // Lane k < K of compute wave c posts into slot c*K + k; r < 0 posts nothing.
 template <int K>
@@ -771,7 +868,7 @@ __host__ __device__ inline int pen_floats(int V, int W) { return ((V + W - 1) / 
 template <int TYPE>
 struct B1Item {
     Pre<TYPE, FQ> pc;
-    float qb;  // communication lanes: the bias of their row
+    float qc, qe;  // communication lanes: their row's folded LN2 constants (bias in qe)
 };
 template <int TYPE>
 struct B1Side {
@@ -805,7 +902,8 @@ template <int TYPE>
 __device__ __forceinline__ void b1_item_prefetch(B1Item<TYPE> &S, const MegaLayer *ls, int l, bool item, int cq0,
                                                  int cq1, int nbd) {
     const MegaLayer &Ly = ls[l];
-    S.qb = item ? comm_bias(glob<gf>(Ly.cqb), cq0, cq1) : 0.0f;
+    S.qc = item ? comm_bias(glob<gf>(Ly.cqc), cq0, cq1) : 0.0f;
+    S.qe = item ? comm_bias(glob<gf>(Ly.cqe), cq0, cq1) : 0.0f;
     flat_prefetch<TYPE, FQ>(S.pc, uview(Ly.cq), nbd, cq0, cq1 - cq0, item);
 }
 
@@ -860,6 +958,17 @@ __device__ __forceinline__ void chunk_rows(float4 (&r)[PVK], const float *base, 
     }
 }
 
+// An item's V rows for C (chunk_rows), zeros for other workgroups.
+__device__ __forceinline__ void v_rows(float4 (&r)[PVK], bool item, const float *base, int enc_len, int ih, int t0,
+                                       int t1) {
+    if (item) {
+        chunk_rows(r, base, enc_len, ih, t0, t1);
+    } else {
+#pragma unroll
+        for (int j = 0; j < PVK; j++) r[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
 template <int TYPE>
 __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
     extern __shared__ __align__(16) float lds[];
@@ -883,6 +992,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
     int *pen = (int *)(sc + 32 * PKV);    // [pen_floats] window counts of this workgroup's vocabulary rows
     float *kst = (float *)pen + pen_floats(a.V, gridDim.x);  // [chunk_len * 64] K rows of this item's chunk
     uint32_t *fil = (uint32_t *)(kst + a.chunk_len * 64);     // [3][NT] flat-split constants by thread
+    float *lnf = (float *)(fil + 3 * NT);                      // [2][d] final LayerNorm weight, bias
     __shared__ float eotv;
     __shared__ int eotf;
 
@@ -913,6 +1023,10 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
     fil[tid()] = flat_info<FQ, RQ>(nbd, has_item ? cq1 - cq0 : 0);
     fil[NT + tid()] = flat_info<FE, RE>(nbd, rf1 - rf0);
     fil[2 * NT + tid()] = flat_info<FF, RF>(nbf, rd1 - rd0);
+    for (int i = tid(); i < d; i += NT) {
+        lnf[i] = a.lnw[i];
+        lnf[d + i] = a.lnb[i];
+    }
 
     unsigned g = a.g0;
     int tok = a.tok0, len = a.len0, prev = a.prev0, streak = a.streak0;
@@ -928,6 +1042,11 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
     prefetch<TYPE, SO, 1>(pS, uview(ls[0].so), nbd, o0, o1);
     if (has_item) stage_k(ls[0].crossK, a.enc_len, ih, t0, t1, kst);
     b1_item_prefetch<TYPE>(nb1, ls, 0, has_item, cq0, cq1, nbd);
+    // V rows of this item's chunk for C (zeros elsewhere), issued a layer ahead with
+    // the K rows: issued later, the wait before the score phase's LDS reads (which the
+    // K rows' direct-to-LDS loads impose) would cover them too
+    float4 vr[PVK];
+    v_rows(vr, has_item, ls[0].crossV, a.enc_len, ih, t0, t1);
 
     for (int step = 0; step < a.n_steps; step++) {
         const int pos = len - 1;
@@ -958,49 +1077,63 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
             float cb;
             // ---------------- B1: cross q rows (items) / side rows ----------------
             TRACE(step, l, 1, 0);
+            // items: x1 = x_l + sa_l (x_0 is local) for LN2, folded into the cross-query
+            // rows (w2*x1 into xn; the statistics during the dots); side workgroups: x_l
+            // LayerNormed (LN1) into xn
+            float x1[XD];
             if (comm()) {
-                // x_l (x_0 is local) and, for items, x1 = x_l + sa_l, LayerNormed into xn:
-                // LN2 for items, LN1 for side workgroups
-                LnW<XD> lp;
-                if (has_item) ln_params<XD>(lp, glob<gf>(Ly.ln2w), glob<gf>(Ly.ln2b), d);
-                else ln_params<XD>(lp, glob<gf>(Ly.ln1w), glob<gf>(Ly.ln1b), d);
-                if (l > 0) {
-                    if (has_item) ll_load_ln<XD, true>(xn, a.xg, d, gin, a.err, lp, sav);
-                    else ll_load_ln<XD, false>(xn, a.xg, d, gin, a.err, lp, nullptr);
-                } else {
-                    ll_load<XD, false>(sav, a.sa, d, gin, a.err);
-                    const int lane = tid() & 63;
-                    float x[XD];
+                if (has_item) {
+                    float w2[XD];
+                    ln_gain<XD>(w2, glob<gf>(Ly.ln2w), d);
+                    if (l > 0) {
+                        ll_load_scaled<XD, true>(x1, xn, a.xg, d, gin, a.err, w2, sav);
+                    } else {
+                        ll_load<XD, false>(sav, a.sa, d, gin, a.err);
+                        const int lane = tid() & 63;
 #pragma unroll
-                    for (int k = 0; k < XD; k++) {
-                        const int i = min(lane + 64 * k, d - 1);
-                        x[k] = has_item ? xs[pad(i)] + sav[i] : xs[pad(i)];
+                        for (int k = 0; k < XD; k++) {
+                            const int i = min(lane + 64 * k, d - 1);
+                            x1[k] = xs[pad(i)] + sav[i];
+                        }
+                        store_scaled<XD>(x1, w2, d, xn);
                     }
-                    ln_wave<XD>(x, d, lp, xn);
+                } else {
+                    LnW<XD> lp;
+                    ln_params<XD>(lp, glob<gf>(Ly.ln1w), glob<gf>(Ly.ln1b), d);
+                    if (l > 0) {
+                        ll_load_ln<XD, false>(xn, a.xg, d, gin, a.err, lp, nullptr);
+                    } else {
+                        const int lane = tid() & 63;
+#pragma unroll
+                        for (int k = 0; k < XD; k++) x1[k] = xs[pad(min(lane + 64 * k, d - 1))];
+                        ln_wave<XD>(x1, d, lp, xn);
+                        ll_load<XD, false>(sav, a.sa, d, gin, a.err);  // sa_0 for D
+                    }
                 }
                 TRACE(step, l, 1, 1);
             }
             __syncthreads();
             ++g;
             const unsigned gB1 = g;  // items' cross-query rows; side workgroups' sa_{l+1} rows
-            float4 vr[PVK];  // V rows of this item's chunk for C (zeros elsewhere)
             if (has_item) {
+                float mean = 0.0f, rsd = 0.0f;
                 {
                     float out[RQ];
                     flat_dots<TYPE, FQ, RQ>(nb1.pc, fil[tid()], xn, out);
+                    if (comm()) ln_stats<XD>(x1, d, mean, rsd);
                     flat_post<RQ>(obv, out);
                 }
+
                 __syncthreads();
                 TRACE(step, l, 1, 2);
                 if (comm()) {
                     const int t = tid();
-                    if (t < cq1 - cq0) st_pair(&a.qx[cq0 + t], flat_sum(obv, fil[t]) + nb1.qb, gB1);
+                    if (t < cq1 - cq0)
+                        st_pair(&a.qx[cq0 + t], ln_fold(flat_sum(obv, fil[t]), mean, rsd, nb1.qc, nb1.qe), gB1);
                 }
                 prefetch<TYPE, SD, 1, 0>(pd, uview(Ly.co), nbd, 0, 0);  // zeros until C
                 cb = 0.0f;
             } else {
-#pragma unroll
-                for (int j = 0; j < PVK; j++) vr[j] = make_float4(0.f, 0.f, 0.f, 0.f);
                 B1Side<TYPE> sp;
                 b1_side_load<TYPE>(sp, a, ls, l, q0, q1, o0, o1, nbd);
                 v0_store(sp.v0r, v0, d);
@@ -1077,9 +1210,6 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                     for (int i = 1; i < NW; i++) m = fmaxf(m, red[i]);
                     st_pair(&a.cmax[item], m, gB);
                 }
-                // C's V rows, issued after the barrier: issuing 70 KiB of loads keeps the
-                // compute waves busy for a while
-                chunk_rows(vr, Ly.crossV, a.enc_len, ih, t0, t1);
                 TRACEC(step, l, 0, 5);
             }
             // ---------------- C: softmax weights, partial P.V, head combine ----------------
@@ -1169,7 +1299,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
             }
             // ---------------- D: cross out rows -> x2 ----------------
             Pre<TYPE, FE> pe;
-            float fbE;
+            float fcE, feE;
             {
                 TRACE(step, l, 3, 0);
                 if (comm()) {
@@ -1195,7 +1325,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 ++g;
                 if (comm()) flush<SD>(obi, obv, a.x2, g);
                 // E's bias and rows
-                fbE = comm_bias(glob<gf>(Ly.fc1b), rf0, rf1);
+                fcE = comm_bias(glob<gf>(Ly.f1c), rf0, rf1);
+                feE = comm_bias(glob<gf>(Ly.f1e), rf0, rf1);
                 flat_prefetch<TYPE, FE>(pe, uview(Ly.fc1), nbd, rf0, rf1 - rf0, true);
             }
             const unsigned gD = g;
@@ -1204,20 +1335,24 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
             float fbF;
             {
                 TRACE(step, l, 4, 0);
+                // x2 for LN3, folded into the fc1 rows (w3*x2 into xn; the statistics during the dots)
+                float x2v[XD];
                 if (comm()) {
-                    LnW<XD> lp;
-                    ln_params<XD>(lp, glob<gf>(Ly.ln3w), glob<gf>(Ly.ln3b), d);
-                    ll_load_ln<XD, false>(xn, a.x2, d, gD, a.err, lp, nullptr);
+                    float w3[XD];
+                    ln_gain<XD>(w3, glob<gf>(Ly.ln3w), d);
+                    ll_load_scaled<XD, false>(x2v, xn, a.x2, d, gD, a.err, w3, nullptr);
                     TRACE(step, l, 4, 1);
                 }
                 __syncthreads();
                 TRACE(step, l, 4, 3);
                 TRACE(step, l, 4, 4);
                 TRACEC(step, l, 4, 7);
+                float mean = 0.0f, rsd = 0.0f;
                 {
                     float out[RE];
                     flat_dots<TYPE, FE, RE>(pe, fil[NT + tid()], xn, out);
                     TRACEC(step, l, 4, 5);
+                    if (comm()) ln_stats<XD>(x2v, d, mean, rsd);
                     flat_post<RE>(obv, out);
                 }
                 __syncthreads();
@@ -1225,7 +1360,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 ++g;
                 if (comm()) {
                     const int t = tid();
-                    if (t < rf1 - rf0) st_pair(&a.hbuf[rf0 + t], gelu_f32(flat_sum(obv, fil[NT + t]) + fbE), g);
+                    if (t < rf1 - rf0)
+                        st_pair(&a.hbuf[rf0 + t], gelu_f32(ln_fold(flat_sum(obv, fil[NT + t]), mean, rsd, fcE, feE)), g);
                 }
                 TRACE(step, l, 4, 6);
                 // F's bias and rows
@@ -1269,9 +1405,11 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 }
                 TRACE(step, l, 5, 6);
                 if (l + 1 < L) {
-                    // the next layer's K rows (this layer's were consumed in B2), then its B1 rows
+                    // the next layer's K rows (this layer's were consumed in B2), its B1 rows,
+                    // then its V rows (C)
                     if (has_item) stage_k(ls[l + 1].crossK, a.enc_len, ih, t0, t1, kst);
                     b1_item_prefetch<TYPE>(nb1, ls, l + 1, has_item, cq0, cq1, nbd);
+                    v_rows(vr, has_item, ls[l + 1].crossV, a.enc_len, ih, t0, t1);
                 }
             }
         }
@@ -1293,9 +1431,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                     const int id = hl[(start + i) & 127];
                     if (id >= rv0 && id < rv1) atomicAdd(&pen[id - rv0], 1);
                 }
-                LnW<XD> lp;
-                ln_params<XD>(lp, glob<gf>(a.lnw), glob<gf>(a.lnb), d);
-                ll_load_ln<XD, false>(xn, a.xg, d, gF, a.err, lp, nullptr);
+                // the final LayerNorm's parameters come from LDS: registers are short here
+                ll_load_ln_lds<XD>(xn, a.xg, d, gF, a.err, lnf, lnf + d);
                 TRACE(step, L, 6, 1);
             }
             __syncthreads();
@@ -1371,6 +1508,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
             prefetch<TYPE, SO, 1>(pS, uview(ls[0].so), nbd, o0, o1);
             if (has_item) stage_k(ls[0].crossK, a.enc_len, ih, t0, t1, kst);
             b1_item_prefetch<TYPE>(nb1, ls, 0, has_item, cq0, cq1, nbd);
+            v_rows(vr, has_item, ls[0].crossV, a.enc_len, ih, t0, t1);
             g = gT;
             __syncthreads();
             tok = __float_as_int(red[63]);
@@ -1408,7 +1546,7 @@ extern "C" int wh_mega_trace_read(void *out, size_t bytes) {
 size_t lds_bytes(int d, int L, int V, int W, int chunk_len) {
     const int d36 = ((d + 31) / 32) * 36;
     return sizeof(float) * (size_t)(layer_floats(L) + 6 * d36 + d + 64 * 4 + 2 * OUTBOX + 64 * XT + 128 +
-                                    32 * PKV + pen_floats(V, W) + chunk_len * 64 + 3 * NT);
+                                    32 * PKV + pen_floats(V, W) + chunk_len * 64 + 3 * NT + 2 * d);
 }
 
 int launch_decode(uint32_t type, int grid, const MegaArgs &a, hipStream_t st) {

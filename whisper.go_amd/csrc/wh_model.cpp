@@ -140,6 +140,48 @@ int load_vector(const Table &tab, const std::string &name, VecArena &arena, floa
     return arena.add(f, slot);
 }
 
+// Row constants of a LayerNorm folded into the matrix w that reads its output:
+// c = w·g (g the LayerNorm weight) and e = w·b + bias, by the quantised GEMV.
+int fold_rows(const DevMat &w, const float *g, const float *b, const float *bias, int d, float *c, float *e) {
+    const DevMat *mat = &w;
+    GemvIn in{g, d};
+    GemvOut out;
+    out.y = c;
+    out.ldy = w.rows;
+    int rc = launch_gemv(&mat, &in, &out, 1, 1, nullptr);
+    if (rc) return rc;
+    GemvIn in2{b, d};
+    GemvOut out2;
+    out2.y = e;
+    out2.ldy = w.rows;
+    out2.bias = bias;
+    return launch_gemv(&mat, &in2, &out2, 1, 1, nullptr);
+}
+
+// The folded LayerNorm constants of LN2 (cross query rows) and LN3 (fc1 rows)
+// of every layer, when those matrices are quantised (the persistent decode
+// kernel's condition); computed once at load.
+int fold_layernorms(wh_model &m) {
+    const int d = m.n_state;
+    for (const Layer &l : m.layers)
+        if (!is_quant_type(l.cq.type) || !is_quant_type(l.fc1.type)) return WH_OK;
+    const size_t per = 2 * (size_t)d + 2 * 4 * (size_t)d;
+    WH_HIP(hipMalloc(&m.fold_alloc, per * m.layers.size() * sizeof(float)));
+    for (size_t i = 0; i < m.layers.size(); i++) {
+        Layer &l = m.layers[i];
+        float *base = (float *)m.fold_alloc + per * i;
+        l.cqc = base;
+        l.cqe = base + d;
+        l.f1c = base + 2 * d;
+        l.f1e = base + 6 * d;
+        int rc;
+        if ((rc = fold_rows(l.cq, l.ln2w, l.ln2b, l.cqb, d, l.cqc, l.cqe))) return rc;
+        if ((rc = fold_rows(l.fc1, l.ln3w, l.ln3b, l.fc1b, d, l.f1c, l.f1e))) return rc;
+    }
+    WH_HIP(hipDeviceSynchronize());
+    return WH_OK;
+}
+
 }  // namespace
 
 void model_free(wh_model *m) {
@@ -150,6 +192,7 @@ void model_free(wh_model *m) {
         for (DevMat *d : ms) devmat_free(*d);
     }
     if (m->vec_alloc) (void)hipFree(m->vec_alloc);
+    if (m->fold_alloc) (void)hipFree(m->fold_alloc);
     delete m;
 }
 
@@ -275,6 +318,7 @@ int model_create(const wh_tensor *tensors, int32_t n, const wh_meta *meta, int32
     WH_HIP(hipMalloc(&m->vec_alloc, arena.host.size() * sizeof(float) + 256));
     WH_HIP(hipMemcpy(m->vec_alloc, arena.host.data(), arena.host.size() * sizeof(float), hipMemcpyHostToDevice));
     for (auto &f : arena.fix) *f.first = (float *)m->vec_alloc + f.second;
+    if ((rc = fold_layernorms(*m))) return rc;
     // algorithmic weight bytes per token: every matrix once + the tied logits matrix
     uint64_t wb = m->tok.algo_bytes;
     for (auto &l : m->layers) {

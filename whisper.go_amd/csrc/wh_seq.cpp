@@ -264,6 +264,7 @@ int mega_setup(wh_seq &s) {
     if (d / H != 64 || d % 64 != 0 || !is_quant_type(m.tok.type)) return WH_OK;
     for (const Layer &l : m.layers) {
         if (!l.sqkv.alloc) return WH_OK;  // q, k, v not stacked (mixed types)
+        if (!l.cqc || !l.f1c) return WH_OK;  // no folded LayerNorm constants
         const DevMat *ms[] = {&l.sqkv, &l.so, &l.cq, &l.co, &l.fc1, &l.fc2};
         for (const DevMat *x : ms)
             if (x->type != m.tok.type) return WH_OK;
@@ -347,6 +348,7 @@ int mega_setup(wh_seq &s) {
         x.fc2 = view(l.fc2);
         x.ln1w = l.ln1w; x.ln1b = l.ln1b; x.svb = l.svb; x.sob = l.sob; x.ln2w = l.ln2w; x.ln2b = l.ln2b;
         x.cqb = l.cqb; x.cob = l.cob; x.ln3w = l.ln3w; x.ln3b = l.ln3b; x.fc1b = l.fc1b; x.fc2b = l.fc2b;
+        x.cqc = l.cqc; x.cqe = l.cqe; x.f1c = l.f1c; x.f1e = l.f1e;
         x.crossK = s.crossK + (size_t)li * s.enc_len * d;
         x.crossV = s.crossV + (size_t)li * s.enc_len * d;
         x.kv = s.kv + (size_t)li * s.kv_layer;
