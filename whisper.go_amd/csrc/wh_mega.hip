@@ -925,10 +925,22 @@ __device__ __forceinline__ void b1_side_load(B1Side<TYPE> &S, const MegaArgs &a,
     prefetch<TYPE, SO, 1>(S.po, uview(Ln.so), nbd, o0, o1);
 }
 
+// Direct global->LDS load of 16 bytes per lane (lane l writes lds + 16 l bytes;
+// lds wave-uniform), in inline assembly: for the builtin form the compiler makes
+// every later LDS read of the wave wait for all of its outstanding loads, which
+// would hold the next phase's dots until the V rows and weight rows issued with
+// K have arrived. Here the issuing wave waits explicitly (k_wait) before the
+// barrier that precedes the first read. M0 is otherwise unused by this kernel.
+__device__ __forceinline__ void dma16(const float *g, float *lds) {
+    const uint32_t m0v = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float *)lds;
+    __asm__ volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0v)
+                     : "memory", "m0");
+}
+
 // Stage K rows [t0, t1) of head ih (a [enc_len][64] block of crossK) into LDS
-// kst in the same layout with direct global->LDS loads (1 KiB per wave
-// instruction), issued by the compute waves before the weight rows of the
-// next phase: the first wait for those rows then also covers K.
+// kst in the same layout, 1 KiB per instruction, by the compute waves; issued
+// before the next phase's weight rows, so the first wait for those rows also
+// covers K.
 __device__ __forceinline__ void stage_k(const float *crossK, int enc_len, int ih, int t0, int t1, float *kst) {
     const int cw = cwave(), lane = tid() & 63;
     if (cw < 0) return;
@@ -937,10 +949,13 @@ __device__ __forceinline__ void stage_k(const float *crossK, int enc_len, int ih
     const int nblk = (nvec + 63) / 64;
     for (int b = cw; b < nblk; b += NC) {
         const int v = b * 64 + lane;
-        if (v < nvec)
-            __builtin_amdgcn_global_load_lds((void __attribute__((address_space(1))) *)(src + 4 * v),
-                                             (void __attribute__((address_space(3))) *)(kst + b * 256), 16, 0, 0);
+        if (v < nvec) dma16(src + 4 * v, kst + b * 256);
     }
+}
+// The compute waves' wait for their staged K rows (before the barrier that
+// precedes the first read).
+__device__ __forceinline__ void k_wait() {
+    if (!comm()) __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Rows [t0, t1) of head ih of a [enc_len][64] block (cross K or V of one
@@ -1176,6 +1191,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                     ll_load<1, false>(qh, a.qx + ih * 64, 64, gB1, a.err);
                     TRACE(step, l, 0, 1);
                 }
+                k_wait();  // K rows staged in F
                 __syncthreads();
                 TRACEC(step, l, 0, 3);
                 // 16 lanes per key, 4 elements each; key k of the chunk is 32 j + (thread >> 4).
