@@ -145,6 +145,26 @@ def test_beam_tokens_identical(wh, orc, gpu):
     assert dec.decode_tokens(enc, p) == ref.decode(enc, p)
 
 
+def test_beam_tied_logits(wh, orc, gpu):
+    """Token-embedding rows repeated with period 7 give every logit value ~170
+    times (the logits matrix is the embedding), so every step's top-k holds
+    equal values: the kept tokens and their order are those of the reference's
+    replace-min scan (decoder.go:1089-1127), which the device reruns for such
+    rows, not the (value, index) order of the plain top-k."""
+    tensors, meta = _model(wh, "beamtie", 7, (1200, 128, 2, 2, 48))
+    for t in tensors:
+        if t.name == "decoder.token_embedding.weight":
+            rows = t.data.reshape(t.shape[0], -1)
+            rows[:] = rows[np.arange(t.shape[0]) % 7]
+    enc = wh.synth.encoder_output("beamtie", 128, enc_len=100)
+    dec = wh.HIPDecoder(tensors, meta)
+    ref = orc.OracleModel(tensors, meta)
+    p = wh.DecoderParams(prompt=[5, 6, 7], beam_size=5, max_tokens=12, no_fallback=True)
+    got = dec.decode_tokens(enc, p)
+    assert got == ref.decode(enc, p)
+    assert len(got) > 3
+
+
 def test_batch_equals_single_streams(wh, orc, gpu):
     tensors, meta = _model(wh, "batch", 3, (1000, 128, 2, 2, 64))
     dec = wh.HIPDecoder(tensors, meta)

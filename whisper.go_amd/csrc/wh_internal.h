@@ -152,6 +152,14 @@ int launch_penalty_argmax(const float *logits, const int32_t *hist, const int32_
 int launch_argmax_final(const SampleBufs &b, const float *cur, int S, int V, int eot, int suppress_nst,
                         float no_speech_thold, const int32_t *active, int32_t *hist, int32_t *hist_len,
                         int hist_cap, int32_t *tok, int32_t *pos, int32_t *out_ids, hipStream_t st);
+// Exact top-k of rows whose k_topk result has ties (the reference's replace-min scan).
+int launch_topk_ties(const float *cur, const int32_t *active, int S, int V, int k, int kk, float inv_temp,
+                     const float *logz, int32_t *tok, float *lp, hipStream_t st);
+// One beam step's candidate ranking, prune and history rewrite on the device.
+int launch_beam_select(const int32_t *ttok, const float *tlp, int k, int kk, const int32_t *hist_in,
+                       const int32_t *len_in, int32_t *hist_out, int32_t *len_out, int cap, float *score,
+                       int32_t *nbeams, int32_t *active, int32_t *tok, int32_t *pos, int32_t *stop,
+                       const float *powtab, int bs, int eot, hipStream_t st);
 int launch_topk(const float *cur, const int32_t *active, int S, int V, int k, float inv_temp, int32_t *out_tok,
                 float *out_lp, float *out_logz, hipStream_t st);
 

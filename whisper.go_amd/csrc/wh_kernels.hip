@@ -890,6 +890,7 @@ int launch_argmax_final(const SampleBufs &b, const float *cur, int S, int V, int
 // One block per stream.
 // ---------------------------------------------------------------------------
 constexpr int TOPK_MAX = 8;
+constexpr int BEAM_MAX = 16;
 
 __global__ __launch_bounds__(256) void k_topk(const float *cur, const int32_t *active, int V, int k, float inv_temp,
                                               int32_t *out_tok, float *out_lp, float *out_logz) {
@@ -965,6 +966,183 @@ __global__ __launch_bounds__(256) void k_topk(const float *cur, const int32_t *a
         out_lp[(size_t)s * k + threadIdx.x] = selv[threadIdx.x] - logz;
     }
     if (threadIdx.x == 0) out_logz[s] = logz;
+}
+
+// ---------------------------------------------------------------------------
+// Beam-search bookkeeping on the device (internal/model/decoder.go:528-726):
+// the candidates, their order and the next hypotheses never leave the GPU.
+// ---------------------------------------------------------------------------
+
+// Rows of k_topk ([S][kk], kk = k + 1) with equal values at or inside the k-th
+// place: the kept set and its order are those of the reference's streaming
+// replace-min scan (decoder.go:1089-1121) followed by a stable sort by value
+// (decoder.go:1123-1127), so one thread reruns that scan over the penalised row
+// and rewrites the first k entries. Other rows keep k_topk's (value desc, index
+// asc) result, which is the same when no values tie.
+__global__ __launch_bounds__(64) void k_topk_ties(const float *cur, const int32_t *active, int V, int k, int kk,
+                                                  float inv_temp, const float *logz, int32_t *tok, float *lp) {
+    const int s = blockIdx.x;
+    if (threadIdx.x != 0 || (active && !active[s])) return;
+    float *l = lp + (size_t)s * kk;
+    bool tie = false;
+    for (int j = 0; j + 1 < kk; j++) tie |= (l[j] == l[j + 1]);
+    if (!tie) return;
+    const float *x = cur + (size_t)s * V;
+    int bt[TOPK_MAX], order[TOPK_MAX];
+    float bv[TOPK_MAX];
+    int n = 0, minpos = -1;
+    float minval = 0.0f;
+    for (int i = 0; i < V; i++) {
+        const float sc = x[i] * inv_temp;
+        if (n < k) {
+            bt[n] = i;
+            bv[n] = sc;
+            if (minpos < 0 || sc < minval) { minpos = n; minval = sc; }
+            n++;
+            continue;
+        }
+        if (sc <= minval) continue;
+        bt[minpos] = i;
+        bv[minpos] = sc;
+        minpos = 0;
+        minval = bv[0];
+        for (int j = 1; j < n; j++)
+            if (bv[j] < minval) { minval = bv[j]; minpos = j; }
+    }
+    const float lz = logz[s];
+    for (int j = 0; j < n; j++) {
+        bv[j] -= lz;
+        order[j] = j;
+    }
+    for (int a = 1; a < n; a++) {  // stable insertion sort, value descending
+        const int o = order[a];
+        int b = a - 1;
+        while (b >= 0 && bv[order[b]] < bv[o]) {
+            order[b + 1] = order[b];
+            b--;
+        }
+        order[b + 1] = o;
+    }
+    int32_t *t = tok + (size_t)s * kk;
+    for (int j = 0; j < k; j++) {
+        t[j] = j < n ? bt[order[j]] : -1;
+        l[j] = j < n ? bv[order[j]] : 0.0f;
+    }
+}
+
+// One beam step's prune (decoder.go:578-660): every live hypothesis b < *nbeams
+// proposes its k candidates (score + logprob, normalised by len^0.6 with len the
+// new length), a finished one (last token EOT) proposes itself; candidates are
+// ranked by normalised score, descending, ties in proposal order (a stable sort;
+// Go's sort.Slice is not stable, the order among exact ties is a documented
+// choice), the first bs become the next hypotheses. Their histories go to the
+// other history buffer; the current token, position, activity, score and count
+// are updated in place, and *stop is set when every hypothesis has finished or
+// the first one repeats its last token more than 20 times (decoder.go:703-718).
+// powtab[n] = float(pow(n, 0.6)) as the host computes it. A stopped state is left
+// as it is.
+__global__ __launch_bounds__(256) void k_beam_select(const int32_t *ttok, const float *tlp, int k, int kk,
+                                                     const int32_t *hist_in, const int32_t *len_in,
+                                                     int32_t *hist_out, int32_t *len_out, int cap, float *score,
+                                                     int32_t *nbeams, int32_t *active, int32_t *tok, int32_t *pos,
+                                                     int32_t *stop, const float *powtab, int bs, int eot) {
+    __shared__ float cnorm[BEAM_MAX * TOPK_MAX], cscore[BEAM_MAX * TOPK_MAX], clp[BEAM_MAX * TOPK_MAX];
+    __shared__ int cpar[BEAM_MAX * TOPK_MAX], ctok[BEAM_MAX * TOPK_MAX];
+    __shared__ int sel[BEAM_MAX];
+    __shared__ int ncand, nkeep;
+    const int t = threadIdx.x;
+    if (*stop) return;
+    if (t == 0) {
+        const int nb = *nbeams;
+        int n = 0;
+        for (int b = 0; b < nb; b++) {
+            const int L = len_in[b];
+            const int last = L > 0 ? hist_in[(size_t)b * cap + L - 1] : -1;
+            const float sc = score[b];
+            if (last == eot) {
+                cpar[n] = b; cscore[n] = sc; ctok[n] = eot; clp[n] = 0.0f; cnorm[n] = sc / powtab[L];
+                n++;
+            } else {
+                for (int c = 0; c < k; c++) {
+                    const float lpc = tlp[(size_t)b * kk + c];
+                    const float ns = sc + lpc;
+                    cpar[n] = b; cscore[n] = ns; ctok[n] = ttok[(size_t)b * kk + c]; clp[n] = lpc;
+                    cnorm[n] = ns / powtab[L + 1];
+                    n++;
+                }
+            }
+        }
+        ncand = n;
+        nkeep = min(n, bs);
+    }
+    if (t < BEAM_MAX) sel[t] = 0;  // every kept slot is written below; a NaN score cannot leave one unset
+    __syncthreads();
+    const int n = ncand, keep = nkeep;
+    if (t < n) {
+        const float v = cnorm[t];
+        int r = 0;
+        for (int j = 0; j < n; j++) r += (cnorm[j] > v) || (cnorm[j] == v && j < t);
+        if (r < keep) sel[r] = t;
+    }
+    __syncthreads();
+    for (int r = 0; r < keep; r++) {
+        const int c = sel[r], par = cpar[c];
+        const int L = len_in[par];
+        for (int j = t; j < L; j += blockDim.x) hist_out[(size_t)r * cap + j] = hist_in[(size_t)par * cap + j];
+    }
+    if (t == 0) {
+        for (int r = 0; r < keep; r++) {
+            const int c = sel[r], par = cpar[c];
+            const int L = len_in[par];
+            const int last = L > 0 ? hist_in[(size_t)par * cap + L - 1] : -1;
+            // a finished hypothesis carried over keeps its tokens (decoder.go:644-651)
+            const bool carry = last == eot && ctok[c] == eot && clp[c] == 0.0f;
+            const int Ln = carry ? L : L + 1;
+            if (!carry) hist_out[(size_t)r * cap + L] = ctok[c];
+            const int lt = carry ? last : ctok[c];
+            len_out[r] = Ln;
+            score[r] = cscore[c];
+            tok[r] = lt;
+            pos[r] = Ln - 1;
+            active[r] = lt != eot;
+        }
+        for (int r = keep; r < bs; r++) active[r] = 0;
+        *nbeams = keep;
+    }
+    __syncthreads();
+    if (t == 0) {
+        bool all = true;
+        for (int r = 0; r < keep; r++) all &= (tok[r] == eot);
+        bool halt = all || keep == 0;
+        const int L0 = keep > 0 ? len_out[0] : 0;
+        if (!halt && L0 >= 2) {
+            const int32_t *h0 = hist_out;
+            int streak = 1;
+            for (int i = L0 - 2; i >= 0 && h0[i] == h0[L0 - 1]; i--)
+                if (++streak > 20) { halt = true; break; }
+        }
+        *stop = halt ? 1 : 0;
+    }
+}
+
+int launch_topk_ties(const float *cur, const int32_t *active, int S, int V, int k, int kk, float inv_temp,
+                     const float *logz, int32_t *tok, float *lp, hipStream_t st) {
+    if (k < 1 || kk > TOPK_MAX || k >= kk) return fail(WH_ERR_INVALID, "topk: bad k");
+    hipLaunchKernelGGL(k_topk_ties, dim3(S), dim3(64), 0, st, cur, active, V, k, kk, inv_temp, logz, tok, lp);
+    WH_HIP(hipGetLastError());
+    return WH_OK;
+}
+
+int launch_beam_select(const int32_t *ttok, const float *tlp, int k, int kk, const int32_t *hist_in,
+                       const int32_t *len_in, int32_t *hist_out, int32_t *len_out, int cap, float *score,
+                       int32_t *nbeams, int32_t *active, int32_t *tok, int32_t *pos, int32_t *stop,
+                       const float *powtab, int bs, int eot, hipStream_t st) {
+    if (bs < 1 || bs > BEAM_MAX || k < 1 || k >= kk || kk > TOPK_MAX || BEAM_MAX * k > 256)
+        return fail(WH_ERR_INVALID, "beam: unsupported beam size");
+    hipLaunchKernelGGL(k_beam_select, dim3(1), dim3(256), 0, st, ttok, tlp, k, kk, hist_in, len_in, hist_out, len_out,
+                       cap, score, nbeams, active, tok, pos, stop, powtab, bs, eot);
+    WH_HIP(hipGetLastError());
+    return WH_OK;
 }
 
 int launch_topk(const float *cur, const int32_t *active, int S, int V, int k, float inv_temp, int32_t *out_tok,

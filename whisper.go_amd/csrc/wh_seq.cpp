@@ -906,83 +906,94 @@ int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, 
 
 // decoder.go:528-726. The beam_size hypotheses run as one batch; every
 // hypothesis is reset before its forward (P9), the cross K/V are shared and
-// computed once (the reference recomputes identical values each step).
-// Candidates are ordered by normalised score with a stable tie-break
-// (insertion order) where Go's sort.Slice is unstable.
+// computed once (the reference recomputes identical values each step). The
+// bookkeeping runs on the device: top-k with log-normaliser (k_topk, plus the
+// reference's scan for rows with ties), candidate ranking by normalised score
+// (a stable order among exact ties where Go's sort.Slice is unstable), the
+// prune and the next hypotheses' histories (k_beam_select). The host reads one
+// stop flag per step.
 int decode_beam(const wh_model *m, const float *enc, int32_t enc_len, int32_t enc_dim, const wh_decode_params *p,
                 int32_t *out_tokens, int32_t cap, int32_t *out_len, const volatile int32_t *cancel) {
     int rc;
     if ((rc = check_params(*m, p))) return rc;
     const float temp = p->temperature == 0 ? 1.0f : p->temperature;
+    const float inv = temp > 0 ? 1.0f / temp : 1.0f;
     const int bs = std::min(p->beam_size <= 0 ? 1 : p->beam_size, 16);
     const int mt = cap_max_tokens(*m, *p);
+    const int P = p->prompt_len;
+    const int eot = m->eot;
+    if (mt <= 0 || (P > 0 && p->prompt[P - 1] == eot)) {
+        // no step runs, or every hypothesis is finished from the start: the first is the prompt
+        if (P > cap) return fail(WH_ERR_INVALID, "model: decode: output capacity too small");
+        if (P > 0) std::memcpy(out_tokens, p->prompt, sizeof(int32_t) * P);
+        *out_len = P;
+        return WH_OK;
+    }
+    if (P == 0) return fail(WH_ERR_INVALID, "model: decode: beam search forward: no tokens in state");
     std::vector<const float *> encs(bs, enc);
     wh_seq *sp = nullptr;
     if ((rc = seq_create(m, bs, encs.data(), enc_len, enc_dim, 1, &sp))) return rc;
     std::unique_ptr<wh_seq, void (*)(wh_seq *)> s(sp, seq_destroy);
-    struct Beam { std::vector<int32_t> tokens; float score; };
-    struct Cand { int parent; float score; int32_t token; float logprob; float norm; };
-    std::vector<Beam> beams(bs, Beam{std::vector<int32_t>(p->prompt, p->prompt + p->prompt_len), 0.0f});
-    std::vector<int32_t> active(bs), ttok((size_t)bs * 5);
-    std::vector<float> tlp((size_t)bs * 5);
+    wh_seq &q = *s;
+    const int hc = q.hist_cap, V = m->n_vocab, K = 5, KK = K + 1;
+    if (P + mt > hc) return fail(WH_ERR_INVALID, "model: decode: history capacity exceeded");
+    int32_t *hist_alt = nullptr, *len_alt = nullptr, *nbeams = nullptr, *stop = nullptr;
+    float *score = nullptr, *powtab = nullptr;
+    if ((rc = q.alloc(&hist_alt, (size_t)bs * hc)) || (rc = q.alloc(&len_alt, (size_t)bs)) ||
+        (rc = q.alloc(&nbeams, 1)) || (rc = q.alloc(&stop, 1)) || (rc = q.alloc(&score, (size_t)bs)) ||
+        (rc = q.alloc(&powtab, (size_t)hc + 2)))
+        return rc;
+    WH_HIP(hipSetDevice(m->device));
+    {
+        // every hypothesis starts as the prompt with score 0; len^0.6 as the reference computes it
+        std::vector<float> pw((size_t)hc + 2);
+        for (size_t n = 0; n < pw.size(); n++) pw[n] = (float)std::pow((double)n, 0.6);
+        std::vector<int32_t> h((size_t)bs * hc, 0), len(bs, P), tk(bs, p->prompt[P - 1]), ps(bs, P - 1), act(bs, 1);
+        for (int b = 0; b < bs; b++) std::memcpy(&h[(size_t)b * hc], p->prompt, sizeof(int32_t) * P);
+        const std::vector<float> sc(bs, 0.0f);
+        const int32_t nb0 = bs, st0 = 0;
+        WH_HIP(hipMemcpy(powtab, pw.data(), sizeof(float) * pw.size(), hipMemcpyHostToDevice));
+        WH_HIP(hipMemcpy(q.hist, h.data(), sizeof(int32_t) * h.size(), hipMemcpyHostToDevice));
+        WH_HIP(hipMemcpy(q.hist_len, len.data(), sizeof(int32_t) * bs, hipMemcpyHostToDevice));
+        WH_HIP(hipMemcpy(q.tok, tk.data(), sizeof(int32_t) * bs, hipMemcpyHostToDevice));
+        WH_HIP(hipMemcpy(q.pos, ps.data(), sizeof(int32_t) * bs, hipMemcpyHostToDevice));
+        WH_HIP(hipMemcpy(q.active, act.data(), sizeof(int32_t) * bs, hipMemcpyHostToDevice));
+        WH_HIP(hipMemcpy(score, sc.data(), sizeof(float) * bs, hipMemcpyHostToDevice));
+        WH_HIP(hipMemcpy(nbeams, &nb0, sizeof(int32_t), hipMemcpyHostToDevice));
+        WH_HIP(hipMemcpy(stop, &st0, sizeof(int32_t), hipMemcpyHostToDevice));
+        for (int b = 0; b < bs; b++) q.h_active[b] = 1;  // host mirror: the profiler's byte counts only
+    }
+    const int H = m->n_head, hd = m->n_state / H;
     for (int step = 0; step < mt; step++) {
         if (cancelled(cancel)) return fail(WH_ERR_CANCELLED, "model: decode: beam search cancelled: context canceled");
-        std::vector<Cand> cands;
-        bool any = false;
-        for (int b = 0; b < (int)beams.size(); b++) {
-            const Beam &h = beams[b];
-            active[b] = !(h.tokens.size() > 0 && h.tokens.back() == m->eot);
-            if (active[b]) {
-                if (h.tokens.empty()) return fail(WH_ERR_INVALID, "model: decode: beam search forward: no tokens in state");
-                if ((rc = seq_set_tokens(s.get(), b, h.tokens.data(), (int32_t)h.tokens.size(), 1))) return rc;
-                any = true;
-            }
+        // reset every hypothesis before its forward (P9): under the reference mask only cache row 0 is read
+        if (m->attn_mode == 0) {
+            const int count = bs * m->n_layer * 2 * H;
+            hipLaunchKernelGGL(k_zero_rows, dim3(std::min(count, 1024)), dim3(64), 0, q.st, q.kv,
+                               (size_t)m->n_ctx * hd, count, hd);
+        } else {
+            WH_HIP(hipMemsetAsync(q.kv, 0, q.kv_stream * sizeof(float) * bs, q.st));
         }
-        for (int b = (int)beams.size(); b < bs; b++) active[b] = 0;
-        if (any && (rc = seq_step_topk(s.get(), active.data(), 5, temp, ttok.data(), tlp.data(), nullptr)))
+        WH_HIP(hipGetLastError());
+        if ((rc = seq_forward(q)) ||
+            (rc = launch_penalty_argmax(q.logits, q.hist, q.hist_len, hc, q.active, bs, V, inv, eot, q.sb, q.st)) ||
+            (rc = launch_topk(q.sb.cur, q.active, bs, V, KK, inv, q.topk_tok, q.topk_lp, q.topk_logz, q.st)) ||
+            (rc = launch_topk_ties(q.sb.cur, q.active, bs, V, K, KK, inv, q.topk_logz, q.topk_tok, q.topk_lp, q.st)) ||
+            (rc = launch_beam_select(q.topk_tok, q.topk_lp, K, KK, q.hist, q.hist_len, hist_alt, len_alt, hc, score,
+                                     nbeams, q.active, q.tok, q.pos, stop, powtab, bs, eot, q.st)))
             return fail(rc, std::string("model: decode: beam search forward: ") + wh_last_error());
-        for (int b = 0; b < (int)beams.size(); b++) {
-            const Beam &h = beams[b];
-            if (!active[b]) {
-                const float norm = h.score / (float)std::pow((double)h.tokens.size(), 0.6);
-                cands.push_back({b, h.score, m->eot, 0.0f, norm});
-                continue;
-            }
-            const int nl = (int)h.tokens.size() + 1;
-            for (int c = 0; c < 5; c++) {
-                const float ns = h.score + tlp[(size_t)b * 5 + c];
-                cands.push_back({b, ns, ttok[(size_t)b * 5 + c], tlp[(size_t)b * 5 + c], ns / (float)std::pow((double)nl, 0.6)});
-            }
-        }
-        std::stable_sort(cands.begin(), cands.end(), [](const Cand &a, const Cand &b) { return a.norm > b.norm; });
-        const int keep = std::min<int>((int)cands.size(), bs);
-        std::vector<Beam> next(keep);
-        for (int i = 0; i < keep; i++) {
-            const Cand &c = cands[i];
-            const Beam &par = beams[c.parent];
-            next[i].tokens = par.tokens;
-            const bool carry = !par.tokens.empty() && par.tokens.back() == m->eot && c.token == m->eot && c.logprob == 0;
-            if (!carry) next[i].tokens.push_back(c.token);
-            next[i].score = c.score;
-        }
-        beams.swap(next);
-        bool all_eot = true;
-        for (auto &h : beams)
-            if (h.tokens.empty() || h.tokens.back() != m->eot) { all_eot = false; break; }
-        if (all_eot) break;
-        if (!beams.empty() && beams[0].tokens.size() >= 2) {
-            const auto &t = beams[0].tokens;
-            int streak = 1;
-            bool stop = false;
-            for (int i = (int)t.size() - 2; i >= 0 && t[i] == t.back(); i--)
-                if (++streak > 20) { stop = true; break; }
-            if (stop) break;
-        }
+        std::swap(q.hist, hist_alt);
+        std::swap(q.hist_len, len_alt);
+        WH_HIP(hipMemcpyAsync(q.pinned_ids, stop, sizeof(int32_t), hipMemcpyDeviceToHost, q.st));
+        WH_HIP(hipStreamSynchronize(q.st));
+        if (q.prof) q.prof_resolve();
+        if (q.pinned_ids[0]) break;
     }
-    if (beams.empty()) { *out_len = 0; return WH_OK; }
-    if ((int)beams[0].tokens.size() > cap) return fail(WH_ERR_INVALID, "model: decode: output capacity too small");
-    std::memcpy(out_tokens, beams[0].tokens.data(), beams[0].tokens.size() * sizeof(int32_t));
-    *out_len = (int32_t)beams[0].tokens.size();
+    int32_t len0 = 0;
+    WH_HIP(hipMemcpy(&len0, q.hist_len, sizeof(int32_t), hipMemcpyDeviceToHost));
+    if (len0 > cap) return fail(WH_ERR_INVALID, "model: decode: output capacity too small");
+    WH_HIP(hipMemcpy(out_tokens, q.hist, sizeof(int32_t) * len0, hipMemcpyDeviceToHost));
+    *out_len = len0;
     return WH_OK;
 }
 
