@@ -65,11 +65,12 @@ struct MegaArgs {
 constexpr int THREADS = 512;
 constexpr int WAVES = THREADS / 64;
 constexpr int CWAVES = WAVES - 1;  // waves 1.. hold weight rows; wave 0 polls, exchanges and publishes
-constexpr int PKV = 9;      // scores: 32 keys per pass of 512 threads, 288 keys per chunk at most
+constexpr int PKQ = 2;      // scores: 128 keys per pass of 512 threads, 256 keys per chunk at most
 constexpr int PVK = 10;     // P.V: float4 of V per compute thread, 448 * 10 / 16 = 280 keys at most
-constexpr int CHUNK_MAX = 280;
+constexpr int CHUNK_MAX = 256;
+constexpr int SC_FLOATS = (CHUNK_MAX + 31) / 32 * 32;  // LDS scores of a chunk
 constexpr int CMIN = 5;     // key chunks per head at least
-constexpr int CMAX = 8;     // key chunks per head at most (2240 encoder frames)
+constexpr int CMAX = 8;     // key chunks per head at most (2048 encoder frames)
 constexpr int XD = 21;      // exchange pairs per lane of a d-vector load: n_state <= 1344
 constexpr int XH = 12;      // exchange pairs per compute lane of the 4d-vector load: 4d <= 7*64*12
 constexpr int XS = 3;       // exchange pairs per compute lane of a d-vector load: d <= 7*64*3

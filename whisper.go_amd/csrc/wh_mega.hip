@@ -1003,8 +1003,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
     int *obi = (int *)(obv + OUTBOX);     // [OUTBOX] posted rows
     float *xp = (float *)(obi + OUTBOX);  // [64 * XT] a head's chunk sums (leader), argmax partials
     int *hl = (int *)(xp + 64 * XT);      // [128] the last 128 tokens of the history, by position mod 128
-    float *sc = (float *)(hl + 128);      // [32*PKV] scores of this workgroup's chunk
-    int *pen = (int *)(sc + 32 * PKV);    // [pen_floats] window counts of this workgroup's vocabulary rows
+    float *sc = (float *)(hl + 128);      // [SC_FLOATS] scores of this workgroup's chunk
+    int *pen = (int *)(sc + SC_FLOATS);   // [pen_floats] window counts of this workgroup's vocabulary rows
     float *kst = (float *)pen + pen_floats(a.V, gridDim.x);  // [chunk_len * 64] K rows of this item's chunk
     uint32_t *fil = (uint32_t *)(kst + a.chunk_len * 64);     // [3][NT] flat-split constants by thread
     float *lnf = (float *)(fil + 3 * NT);                      // [2][d] final LayerNorm weight, bias
@@ -1194,25 +1194,39 @@ __global__ __launch_bounds__(NT, 1) void k_decode(MegaArgs a) {
                 k_wait();  // K rows staged in F
                 __syncthreads();
                 TRACEC(step, l, 0, 3);
-                // 16 lanes per key, 4 elements each; key k of the chunk is 32 j + (thread >> 4).
-                // Keys past the chunk re-read its last key: they rewrite that key's score and
-                // add nothing new to the maximum.
+                // 4 lanes per key, 16 elements each (four float4 chunks); key k of the chunk is
+                // 128 j + (thread >> 2). A lane reads its chunks rotated by its quarter and by
+                // the key's parity, so the 8 lanes of each LDS cycle (two keys) hit disjoint
+                // banks; q is loaded in the same rotation. Keys past the chunk re-read its last
+                // key: they rewrite that key's score and add nothing new to the maximum.
                 {
                     const int tt = tid();
-                    const int n = t1 - t0, kb = tt >> 4, e4 = tt & 15;
-                    const float4 q4 = ((const float4 *)qh)[e4];
+                    const int n = t1 - t0, kq = tt >> 2, e = tt & 3, rot = e + (kq & 1);
+                    const float4 *q4 = (const float4 *)qh;
                     const float4 *k4 = (const float4 *)kst;
-                    float part[PKV];
+                    float4 qv[4];
 #pragma unroll
-                    for (int j = 0; j < PKV; j++) {
-                        const float4 kr = k4[min(kb + 32 * j, n - 1) * 16 + e4];
-                        part[j] = q4.x * kr.x + q4.y * kr.y + q4.z * kr.z + q4.w * kr.w;
+                    for (int m = 0; m < 4; m++) qv[m] = q4[e * 4 + ((m + rot) & 3)];
+                    float part[PKQ];
+#pragma unroll
+                    for (int j = 0; j < PKQ; j++) {
+                        const int key = min(kq + 128 * j, n - 1);
+                        float acc = 0.0f;
+#pragma unroll
+                        for (int m = 0; m < 4; m++) {
+                            const float4 kr = k4[key * 16 + e * 4 + ((m + rot) & 3)];
+                            acc += qv[m].x * kr.x + qv[m].y * kr.y + qv[m].z * kr.z + qv[m].w * kr.w;
+                        }
+                        part[j] = acc;
                     }
                     float mx = -INFINITY;
 #pragma unroll
-                    for (int j = 0; j < PKV; j++) {
-                        const float sj = row_sum16(part[j]) * a.scale;
-                        if (e4 == 0) sc[min(kb + 32 * j, n - 1)] = sj;
+                    for (int j = 0; j < PKQ; j++) {
+                        float v = part[j];
+                        v += dpp<0xB1>(v);  // quad_perm [1,0,3,2]
+                        v += dpp<0x4E>(v);  // quad_perm [2,3,0,1]
+                        const float sj = v * a.scale;
+                        if (e == 0) sc[min(kq + 128 * j, n - 1)] = sj;
                         mx = fmaxf(mx, sj);
                     }
                     mx = wave_max(mx);
@@ -1562,7 +1576,7 @@ extern "C" int wh_mega_trace_read(void *out, size_t bytes) {
 size_t lds_bytes(int d, int L, int V, int W, int chunk_len) {
     const int d36 = ((d + 31) / 32) * 36;
     return sizeof(float) * (size_t)(layer_floats(L) + 6 * d36 + d + 64 * 4 + 2 * OUTBOX + 64 * XT + 128 +
-                                    32 * PKV + pen_floats(V, W) + chunk_len * 64 + 3 * NT + 2 * d);
+                                    SC_FLOATS + pen_floats(V, W) + chunk_len * 64 + 3 * NT + 2 * d);
 }
 
 int launch_decode(uint32_t type, int grid, const MegaArgs &a, hipStream_t st) {

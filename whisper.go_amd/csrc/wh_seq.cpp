@@ -282,7 +282,7 @@ int mega_setup(wh_seq &s) {
                                mega::flat_fits((64 + C - 1) / C, nbd, mega::FQ, mega::RQ)))
         C++;
     const int chunk = (s.enc_len + C - 1) / C;
-    if (s.enc_len < 16 || (C - 1) * chunk >= s.enc_len || chunk > mega::CHUNK_MAX || chunk > 32 * mega::PKV)
+    if (s.enc_len < 16 || (C - 1) * chunk >= s.enc_len || chunk > mega::CHUNK_MAX || chunk > 128 * mega::PKQ)
         return WH_OK;
     const int items = H * C;
     // per-workgroup row capacities of the kernel's register slots (compute waves only)
