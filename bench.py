@@ -17,7 +17,8 @@ Also reported:
   bounded sample of the same workload.
 
 `--gemv` instead runs the standalone quantised-GEMV microbench (rows x cols at
-batch 1 and 5 for each format, rotating over >= 1 GiB of distinct copies).
+batch 1 and 5 for each format, rotating over >= 1 GiB of distinct copies;
+back-to-back launches replayed from a HIP graph, time per launch).
 """
 import argparse
 import json
@@ -194,6 +195,58 @@ def run_decode(args):
     print(json.dumps(out), flush=True)
 
 
+class HipGraphs:
+    """Stream capture into a HIP graph through the HIP runtime the library
+    already loaded (the microbench's launch loop, replayed without Python)."""
+
+    def __init__(self):
+        import ctypes as C
+        path = None
+        with open("/proc/self/maps") as f:
+            for line in f:
+                if "libamdhip64.so" in line:
+                    path = line.split()[-1]
+                    break
+        if path is None:
+            raise RuntimeError("libamdhip64 is not loaded")
+        self.C = C
+        self.h = C.CDLL(path)
+        for n in ("hipStreamBeginCapture", "hipStreamEndCapture", "hipGraphInstantiate", "hipGraphLaunch",
+                  "hipGraphExecDestroy", "hipGraphDestroy"):
+            getattr(self.h, n).restype = C.c_int
+        self.h.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+        self.h.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+        self.h.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]
+        self.h.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+        self.h.hipGraphExecDestroy.argtypes = [C.c_void_p]
+        self.h.hipGraphDestroy.argtypes = [C.c_void_p]
+
+    def _ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed: hipError {rc}")
+
+    def capture(self, stream, issue):
+        C = self.C
+        self._ok(self.h.hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")  # relaxed mode
+        try:
+            rcs = issue()
+        finally:
+            g = C.c_void_p()
+            self._ok(self.h.hipStreamEndCapture(stream, C.byref(g)), "hipStreamEndCapture")
+        if any(rcs):
+            raise RuntimeError(f"launch during capture returned {set(rcs)}")
+        ex = C.c_void_p()
+        self._ok(self.h.hipGraphInstantiate(C.byref(ex), g, None, None, 0), "hipGraphInstantiate")
+        return (g, ex)
+
+    def launch(self, graph, stream):
+        self._ok(self.h.hipGraphLaunch(graph[1], stream), "hipGraphLaunch")
+
+    def destroy(self, graph):
+        self.h.hipGraphExecDestroy(graph[1])
+        self.h.hipGraphDestroy(graph[0])
+
+
 def run_gemv(args):
     """Standalone quantised GEMV at the large-v3 decoder shapes."""
     import ctypes as C
@@ -204,6 +257,7 @@ def run_gemv(args):
     fmts = args.gemv_formats.split(",")
     st = wh.native.Stream()
     e0, e1 = wh.native.Event(), wh.native.Event()
+    hip = HipGraphs()
     rows_out = []
     for fmt in fmts:
         qt = QNAMES[fmt]
@@ -223,15 +277,35 @@ def run_gemv(args):
                 y = wh.native.DevBuf(batch * rows * 4)
                 for h in mats[:4]:
                     wh.native.check(lib.wh_gemv(h, x.ptr, batch, y.ptr, st.h))
-                iters = max(100, ncopy)
-                e0.record(st)
-                for i in range(iters):
+                # back-to-back launches (rotating over the copies) captured in one HIP
+                # graph, timed per graph launch: the kernel plus the gap between
+                # kernels, not the rate at which Python can issue launches; median
+                nlaunch = max(64, ncopy)
+                graph = hip.capture(st.h, lambda: [lib.wh_gemv(mats[i % ncopy], x.ptr, batch, y.ptr, st.h)
+                                                   for i in range(nlaunch)])
+                times = []
+                for rep in range(12):
+                    e0.record(st)
+                    hip.launch(graph, st.h)
+                    e1.record(st)
+                    st.sync()
+                    if rep >= 2:
+                        times.append(e0.elapsed_ms(e1) / nlaunch)
+                hip.destroy(graph)
+                ms = float(np.median(times))
+                # one launch alone between its own pair of events (includes the
+                # launch and event latency)
+                single = []
+                for i in range(32):
+                    e0.record(st)
                     lib.wh_gemv(mats[i % ncopy], x.ptr, batch, y.ptr, st.h)
-                e1.record(st)
-                ms = e0.elapsed_ms(e1) / iters
+                    e1.record(st)
+                    st.sync()
+                    single.append(e0.elapsed_ms(e1))
                 gbs = nbytes / (ms * 1e-3) / 1e9
                 rows_out.append({"format": fmt, "rows": rows, "cols": cols, "batch": batch, "bytes": nbytes,
                                  "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                                 "us_single_launch": round(float(np.median(single)) * 1e3, 3),
                                  "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": ncopy})
                 log(json.dumps(rows_out[-1]))
             for h in mats:

@@ -6,6 +6,7 @@
 // tolerance-based there), except where noted as bit-exact.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
@@ -167,6 +168,412 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Batch-1 quantised GEMV, the streaming form: a wave owns rows in a grid-stride
+// loop and each lane always handles the same blocks (g, g+LG, ... of its group's
+// row), so its 32-element slices of x are loaded into registers once per matrix
+// and reused for every row. The raw blocks of U rows are loaded before any of
+// them is decoded, which keeps U rows of blocks in flight per wave; the
+// codes are converted exactly and s = sum q_i x_i is accumulated in fp32, scaled
+// once by d (plus m * sum x for the _1 formats), as the batched kernel above.
+// LG lanes per row (64/LG rows per wave step), KB = ceil(nb / LG) blocks per lane.
+// ---------------------------------------------------------------------------
+struct RawBlk {
+    uint4 a, b;  // 32 code bytes (Q8_0), or 16 (a) for the 4/5-bit formats
+    uint32_t s, h;  // scale word(s), Q5 high bits
+};
+
+template <int TYPE>
+__device__ __forceinline__ void raw_load(const GemvOpDev &op, size_t blk, RawBlk &r) {
+    if constexpr (TYPE == 8) {
+        const uint4 *p = (const uint4 *)(op.qs + blk * 32);
+        r.a = p[0];
+        r.b = p[1];
+        r.s = ((const uint16_t *)op.sc)[blk];
+        r.h = 0u;
+    } else {
+        r.a = *(const uint4 *)(op.qs + blk * 16);
+        r.b = make_uint4(0u, 0u, 0u, 0u);
+        if constexpr (TYPE == 3 || TYPE == 7) r.s = ((const uint32_t *)op.sc)[blk];
+        else r.s = ((const uint16_t *)op.sc)[blk];
+        if constexpr (TYPE == 6 || TYPE == 7) r.h = op.qh[blk];
+        else r.h = 0u;
+    }
+}
+
+// ---- quantised GEMV with x staged in LDS ----
+// A workgroup stages each batch row of x once as float4 chunks, chunk k (elements
+// 32b+4k..32b+4k+3) of block b at slot 8b + ((k + b) & 7): the LG lanes of a row read
+// LG consecutive blocks at the same k, which fall in distinct banks, and the other
+// rows of the wave read the same slots. LG lanes per weight row, up to KB blocks per
+// lane, one weight row per lane group; its raw blocks are loaded once for the batch.
+constexpr int GEMV2_KB = 5;
+
+__device__ __forceinline__ int xslot(int b, int k) { return 8 * b + ((k + b) & 7); }
+
+// Codes are taken as floats: signed for Q8_0, unsigned for the 4/5-bit formats (the
+// offset, 8 or 16, and the _1 formats' m are applied through sx, the sum of the
+// block's 32 x, by block_scale).
+// the block's contribution from qx = sum q_i x_i and sx = sum x_i
+template <int TYPE>
+__device__ __forceinline__ float block_scale(const RawBlk &r, float qx, float sx) {
+    if constexpr (TYPE == 8) return h2f(r.s) * qx;
+    else if constexpr (TYPE == 2) return h2f(r.s) * __builtin_fmaf(-8.0f, sx, qx);
+    else if constexpr (TYPE == 6) return h2f(r.s) * __builtin_fmaf(-16.0f, sx, qx);
+    else return __builtin_fmaf(h2f(r.s & 0xFFFFu), qx, h2f(r.s >> 16) * sx);
+}
+
+// batch 1: codes made chunk by chunk inside the FMA chains
+template <int TYPE>
+__device__ __forceinline__ float lds_dot(const RawBlk &r, const float4 *xs, int b, float sx) {
+    float acc = 0.0f, acc1 = 0.0f;
+    if constexpr (TYPE == 8) {
+        const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const float4 xv = xs[xslot(b, t)];
+            const int v = (int)w[t];
+            float &c = (t & 1) ? acc1 : acc;
+            c = __builtin_fmaf((float)((v << 24) >> 24), xv.x, c);
+            c = __builtin_fmaf((float)((v << 16) >> 24), xv.y, c);
+            c = __builtin_fmaf((float)((v << 8) >> 24), xv.z, c);
+            c = __builtin_fmaf((float)(v >> 24), xv.w, c);
+        }
+    } else {
+        const uint32_t w[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float4 xa = xs[xslot(b, 2 * t)], xb = xs[xslot(b, 2 * t + 1)];
+            uint32_t lo = w[t] & 0x0F0F0F0Fu, hi = (w[t] >> 4) & 0x0F0F0F0Fu;
+            if constexpr (TYPE == 6 || TYPE == 7) {
+                const uint32_t hb = (r.h >> (8 * t)) & 0xFFu;
+                lo |= ((hb & 0x55u) * 0x00410410u) & 0x10101010u;
+                hi |= (((hb >> 1) & 0x55u) * 0x00410410u) & 0x10101010u;
+            }
+            float &c = (t & 1) ? acc1 : acc;
+            c = __builtin_fmaf((float)(lo & 0xFFu), xa.x, c);
+            c = __builtin_fmaf((float)(hi & 0xFFu), xa.y, c);
+            c = __builtin_fmaf((float)((lo >> 8) & 0xFFu), xa.z, c);
+            c = __builtin_fmaf((float)((hi >> 8) & 0xFFu), xa.w, c);
+            c = __builtin_fmaf((float)((lo >> 16) & 0xFFu), xb.x, c);
+            c = __builtin_fmaf((float)((hi >> 16) & 0xFFu), xb.y, c);
+            c = __builtin_fmaf((float)(lo >> 24), xb.z, c);
+            c = __builtin_fmaf((float)(hi >> 24), xb.w, c);
+        }
+    }
+    return block_scale<TYPE>(r, acc + acc1, sx);
+}
+
+// Batch 1: one weight row per lane group, all of x staged (nb * 132 bytes of LDS).
+template <int TYPE, int LG>
+__global__ __launch_bounds__(256) void k_gemv1(GemvArgs a) {
+    constexpr int KB = GEMV2_KB, GPW = 64 / LG;
+    extern __shared__ float4 xs[];  // 8 * nb chunks, then the nb block sums
+    const GemvOpDev &op = a.op[blockIdx.y];
+    const int nb = op.nb;
+    const int row0 = blockIdx.x * 4 * GPW;
+    if (row0 >= op.rows) return;  // the whole workgroup: past this op's rows
+    const int lane = threadIdx.x & 63, gl = lane % LG;
+    const int row = row0 + (threadIdx.x >> 6) * GPW + lane / LG;
+    const int r = min(row, op.rows - 1);  // past the last row: re-read it, drop it
+    // the weights first: their loads are in flight while x is staged
+    RawBlk blk[KB];
+#pragma unroll
+    for (int k = 0; k < KB; k++)
+        if (LG * k < nb) raw_load<TYPE>(op, (size_t)r * nb + min(gl + LG * k, nb - 1), blk[k]);
+    const int nch = 8 * nb;
+    float *sxs = (float *)(xs + nch);
+    const bool vec = (((uintptr_t)op.x) & 15) == 0;
+    for (int c = threadIdx.x; c < nch; c += 256) {
+        const int e = 4 * c;
+        float4 v;
+        if (vec && e + 3 < op.cols) {
+            v = ((const float4 *)op.x)[c];
+        } else {
+            v.x = e < op.cols ? op.x[e] : 0.0f;
+            v.y = e + 1 < op.cols ? op.x[e + 1] : 0.0f;
+            v.z = e + 2 < op.cols ? op.x[e + 2] : 0.0f;
+            v.w = e + 3 < op.cols ? op.x[e + 3] : 0.0f;
+        }
+        xs[xslot(c >> 3, c & 7)] = v;
+    }
+    __syncthreads();
+    if constexpr (TYPE != 8) {
+        for (int b = threadIdx.x; b < nb; b += 256) {
+            float s = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const float4 v = xs[xslot(b, k)];
+                s += (v.x + v.y) + (v.z + v.w);
+            }
+            sxs[b] = s;
+        }
+        __syncthreads();
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KB; k++) {
+        const int b = gl + LG * k;
+        if (b < nb) acc += lds_dot<TYPE>(blk[k], xs, b, TYPE == 8 ? 0.0f : sxs[b]);
+    }
+    acc = group_sum<LG>(acc);
+    if (gl == 0 && row < op.rows) {
+        float v = acc;
+        if (op.bias) v = v + op.bias[row];
+        if (op.gelu) v = gelu_ref(v);
+        if (op.res) v = op.res[row] + v;
+        op.y[row] = v;
+    }
+}
+
+// codes of elements 4c..4c+3 of one raw block (c = 0..7), as block_codes makes them
+template <int TYPE>
+__device__ __forceinline__ void chunk_codes(const RawBlk &r, int c, float (&q)[4]) {
+    if constexpr (TYPE == 8) {
+        const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+        const int v = (int)w[c];
+        q[0] = (float)((v << 24) >> 24);
+        q[1] = (float)((v << 16) >> 24);
+        q[2] = (float)((v << 8) >> 24);
+        q[3] = (float)(v >> 24);
+    } else {
+        const uint32_t w[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+        const int t = c >> 1, sh = 16 * (c & 1);  // bytes 2c, 2c + 1: word c / 2
+        uint32_t lo = w[t] & 0x0F0F0F0Fu, hi = (w[t] >> 4) & 0x0F0F0F0Fu;
+        if constexpr (TYPE == 6 || TYPE == 7) {
+            const uint32_t hb = (r.h >> (8 * t)) & 0xFFu;
+            lo |= ((hb & 0x55u) * 0x00410410u) & 0x10101010u;
+            hi |= (((hb >> 1) & 0x55u) * 0x00410410u) & 0x10101010u;
+        }
+        q[0] = (float)((lo >> sh) & 0xFFu);
+        q[1] = (float)((hi >> sh) & 0xFFu);
+        q[2] = (float)((lo >> (sh + 8)) & 0xFFu);
+        q[3] = (float)((hi >> (sh + 8)) & 0xFFu);
+    }
+}
+
+// the raw words through an empty asm statement: codes made from the copy are made
+// where they are used, not hoisted out of the chunk loop for all blocks at once
+template <int TYPE>
+__device__ __forceinline__ RawBlk opaque_blk(const RawBlk &b) {
+    RawBlk r = b;
+    asm volatile("" : "+v"(r.a.x), "+v"(r.a.y), "+v"(r.a.z), "+v"(r.a.w));
+    if constexpr (TYPE == 8) asm volatile("" : "+v"(r.b.x), "+v"(r.b.y), "+v"(r.b.z), "+v"(r.b.w));
+    if constexpr (TYPE == 6 || TYPE == 7) asm volatile("" : "+v"(r.h));
+    return r;
+}
+
+// A batch of up to NB rows of x (the rows from batch to NB staged as zeros): two
+// adjacent weight rows per lane group, so each x chunk read from LDS feeds both.
+template <int TYPE, int LG, int NB>
+__global__ __launch_bounds__(256) void k_gemv2(GemvArgs a, int ch) {
+    constexpr int KB = GEMV2_KB, GPW = 64 / LG, RW = 2, XR = 4;
+    // per batch row m: 8 * ch chunks of x, then ch block sums
+    extern __shared__ float4 xs[];
+    const GemvOpDev &op = a.op[blockIdx.y];
+    const int nb = op.nb, batch = a.batch;
+    const int row0 = blockIdx.x * 4 * GPW * RW;
+    if (row0 >= op.rows) return;  // the whole workgroup: past this op's rows
+    const int lane = threadIdx.x & 63, gl = lane % LG;
+    const int row = row0 + ((threadIdx.x >> 6) * GPW + lane / LG) * RW;
+    const int stride = 8 * ch + ch / 4;  // float4s per batch row (ch is a multiple of 4)
+    const bool vec = (((uintptr_t)op.x) & 15) == 0 && (op.ldx & 3) == 0 && (op.cols & 3) == 0;
+    // x is staged in rounds of up to XR float4 chunks per thread, all of a round's
+    // loads before its stores; the first round is loaded before the weights (x is
+    // small and cached, and no wait for the weights stands before its loads). x not
+    // 16-byte aligned, or cols not a multiple of 4: a plain loop (x_slow) instead.
+    float4 xv[XR];
+    auto x_round = [&](int cb, int i0) {
+        if (!vec) return;
+        const int nch = 8 * min(ch, nb - cb), nall = NB * nch;
+#pragma unroll
+        for (int j = 0; j < XR; j++) {
+            const int i = i0 + 256 * j + threadIdx.x;
+            const int m = i / nch, c = i - m * nch;
+            const int e = 32 * cb + 4 * c;
+            xv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (i < nall && m < batch && e < op.cols) xv[j] = *(const float4 *)(op.x + (size_t)m * op.ldx + e);
+        }
+    };
+    x_round(0, 0);
+    // the weights: in flight while x is staged
+    RawBlk blk[RW][KB];
+#pragma unroll
+    for (int u = 0; u < RW; u++) {
+        const int r = min(row + u, op.rows - 1);  // past the last row: re-read it, drop it
+#pragma unroll
+        for (int k = 0; k < KB; k++)
+            if (LG * k < nb) raw_load<TYPE>(op, (size_t)r * nb + min(gl + LG * k, nb - 1), blk[u][k]);
+    }
+    float acc[RW][NB];
+#pragma unroll
+    for (int u = 0; u < RW; u++)
+#pragma unroll
+        for (int m = 0; m < NB; m++) acc[u][m] = 0.0f;
+    // column chunks of ch blocks (one chunk whenever x fits): ch is a multiple of LG,
+    // so block gl + LG * k of every lane lies in the same chunk
+    for (int cb = 0; cb < nb; cb += ch) {
+        const int nbc = min(ch, nb - cb), nch = 8 * nbc, nall = NB * nch;
+        if (vec) {
+            for (int i0 = 0; i0 < nall; i0 += 256 * XR) {
+                if (cb > 0 || i0 > 0) x_round(cb, i0);
+#pragma unroll
+                for (int j = 0; j < XR; j++) {
+                    const int i = i0 + 256 * j + threadIdx.x;
+                    const int m = i / nch, c = i - m * nch;
+                    if (i < nall) xs[m * stride + xslot(c >> 3, c & 7)] = xv[j];
+                }
+            }
+        } else {
+            for (int i = threadIdx.x; i < 4 * nall; i += 256) {  // x_slow: one float each
+                const int q = i >> 2, m = q / nch, c = q - m * nch, e = 32 * cb + 4 * c + (i & 3);
+                const float v = (m < batch && e < op.cols) ? op.x[(size_t)m * op.ldx + e] : 0.0f;
+                ((float *)(xs + m * stride + xslot(c >> 3, c & 7)))[i & 3] = v;
+            }
+        }
+        __syncthreads();
+        if constexpr (TYPE != 8) {
+            for (int i = threadIdx.x; i < NB * nbc; i += 256) {
+                const int m = i / nbc, b = i - m * nbc;
+                float s = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const float4 v = xs[m * stride + xslot(b, k)];
+                    s += (v.x + v.y) + (v.z + v.w);
+                }
+                ((float *)(xs + m * stride + 8 * ch))[b] = s;
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int k = 0; k < KB; k++) {
+            const int b = gl + LG * k;
+            if (LG * k >= cb && LG * k < cb + ch && b < nb) {
+                const int bl = b - cb;
+                // the sums pass through an empty asm statement that also clobbers
+                // memory: the FMAs of block k - 1 come before it and the LDS reads of
+                // block k after it (likewise per chunk below); the reads of all blocks
+                // and chunks issued together would not fit the registers
+#pragma unroll
+                for (int m = 0; m < NB; m++) asm volatile("" : "+v"(acc[0][m]), "+v"(acc[1][m])::"memory");
+                const RawBlk ra = opaque_blk<TYPE>(blk[0][k]), rb = opaque_blk<TYPE>(blk[1][k]);
+                float pa[NB], pb[NB];
+#pragma unroll
+                for (int m = 0; m < NB; m++) pa[m] = pb[m] = 0.0f;
+#pragma unroll
+                for (int c = 0; c < 8; c++) {
+#pragma unroll
+                    for (int m = 0; m < NB; m++) asm volatile("" : "+v"(pa[m]), "+v"(pb[m])::"memory");
+                    float qa[4], qb[4];
+                    chunk_codes<TYPE>(ra, c, qa);
+                    chunk_codes<TYPE>(rb, c, qb);
+#pragma unroll
+                    for (int m = 0; m < NB; m++) {
+                        const float4 xv = xs[m * stride + xslot(bl, c)];
+                        pa[m] = __builtin_fmaf(qa[0], xv.x, pa[m]);
+                        pb[m] = __builtin_fmaf(qb[0], xv.x, pb[m]);
+                        pa[m] = __builtin_fmaf(qa[1], xv.y, pa[m]);
+                        pb[m] = __builtin_fmaf(qb[1], xv.y, pb[m]);
+                        pa[m] = __builtin_fmaf(qa[2], xv.z, pa[m]);
+                        pb[m] = __builtin_fmaf(qb[2], xv.z, pb[m]);
+                        pa[m] = __builtin_fmaf(qa[3], xv.w, pa[m]);
+                        pb[m] = __builtin_fmaf(qb[3], xv.w, pb[m]);
+                    }
+                }
+#pragma unroll
+                for (int m = 0; m < NB; m++) {
+                    const float sx = TYPE == 8 ? 0.0f : ((const float *)(xs + m * stride + 8 * ch))[bl];
+                    acc[0][m] += block_scale<TYPE>(ra, pa[m], sx);
+                    acc[1][m] += block_scale<TYPE>(rb, pb[m], sx);
+                }
+            }
+        }
+        if (cb + ch < nb) __syncthreads();  // the next chunk overwrites x
+    }
+#pragma unroll
+    for (int u = 0; u < RW; u++) {
+#pragma unroll
+        for (int m = 0; m < NB; m++) {
+            const float s = group_sum<LG>(acc[u][m]);
+            const int rr = row + u;
+            if (m < batch && gl == 0 && rr < op.rows) {
+                float v = s;
+                if (op.bias) v = v + op.bias[rr];
+                if (op.gelu) v = gelu_ref(v);
+                if (op.res) v = op.res[(size_t)m * op.ldres + rr] + v;
+                op.y[(size_t)m * op.ldy + rr] = v;
+            }
+        }
+    }
+}
+
+constexpr int GEMV2_LDS = 64 * 1024;
+
+// Lanes per row: the fewest (a power of two, at least 4) whose GEMV2_KB blocks each
+// cover the row, doubled while the launch would have fewer workgroups than CUs
+// (rows_per_group weight rows per lane group).
+static int gemv2_lanes(int nbmax, int total_rows, int rows_per_group) {
+    int lg = 4;
+    while (lg * GEMV2_KB < nbmax) lg *= 2;
+    while (lg < 64 && (total_rows + 4 * (64 / lg) * rows_per_group - 1) / (4 * (64 / lg) * rows_per_group) < 256) lg *= 2;
+    return lg;
+}
+
+template <int TYPE, int LG>
+static void gemv1_launch_t(const GemvArgs &a, int maxrows, int nbmax, hipStream_t st) {
+    constexpr int rows_per_wg = 4 * (64 / LG);
+    const dim3 grid((maxrows + rows_per_wg - 1) / rows_per_wg, a.nop);
+    hipLaunchKernelGGL((k_gemv1<TYPE, LG>), grid, dim3(256), (size_t)nbmax * (8 * 16 + 4), st, a);
+}
+
+template <int TYPE, int LG, int NB>
+static void gemv2_launch_t(const GemvArgs &a, int maxrows, int ch, hipStream_t st) {
+    constexpr int rows_per_wg = 4 * (64 / LG) * 2;
+    const dim3 grid((maxrows + rows_per_wg - 1) / rows_per_wg, a.nop);
+    const size_t lds = (size_t)NB * (8 * ch + ch / 4) * 16;
+    hipLaunchKernelGGL((k_gemv2<TYPE, LG, NB>), grid, dim3(256), lds, st, a, ch);
+}
+
+template <int TYPE, int NB>
+static void gemv2_launch_nb(const GemvArgs &a, int lg, int maxrows, int ch, hipStream_t st) {
+    switch (lg) {
+    case 4: gemv2_launch_t<TYPE, 4, NB>(a, maxrows, ch, st); break;
+    case 8: gemv2_launch_t<TYPE, 8, NB>(a, maxrows, ch, st); break;
+    case 16: gemv2_launch_t<TYPE, 16, NB>(a, maxrows, ch, st); break;
+    case 32: gemv2_launch_t<TYPE, 32, NB>(a, maxrows, ch, st); break;
+    default: gemv2_launch_t<TYPE, 64, NB>(a, maxrows, ch, st); break;
+    }
+}
+
+// Quantised GEMV with x staged in LDS: batch 1 (x up to 64 * GEMV2_KB blocks) and
+// batches 2..5; anything else is not handled here (k_gemv takes it).
+template <int TYPE>
+static bool gemv2_launch(const GemvArgs &a, int maxrows, int nbmax, hipStream_t st) {
+    if (nbmax > 64 * GEMV2_KB || a.batch > 5) return false;
+    if (a.batch == 1) {
+        switch (gemv2_lanes(nbmax, a.total_rows, 1)) {
+        case 4: gemv1_launch_t<TYPE, 4>(a, maxrows, nbmax, st); break;
+        case 8: gemv1_launch_t<TYPE, 8>(a, maxrows, nbmax, st); break;
+        case 16: gemv1_launch_t<TYPE, 16>(a, maxrows, nbmax, st); break;
+        case 32: gemv1_launch_t<TYPE, 32>(a, maxrows, nbmax, st); break;
+        default: gemv1_launch_t<TYPE, 64>(a, maxrows, nbmax, st); break;
+        }
+        return true;
+    }
+    const int nb_rows = a.batch == 2 ? 2 : 5;  // rows past the batch are staged as zeros
+    const int lg = gemv2_lanes(nbmax, a.total_rows, 2);
+    const int per_block = nb_rows * (8 * 16 + 4);  // LDS bytes per block of x
+    int ch = ((nbmax + 3) / 4) * 4;
+    if (ch * per_block > GEMV2_LDS) {
+        // several chunks: each a multiple of LG blocks (one chunk may be any width)
+        ch = (GEMV2_LDS / per_block) / lg * lg;
+        if (ch < lg) return false;
+    }
+    if (nb_rows == 2) gemv2_launch_nb<TYPE, 2>(a, lg, maxrows, ch, st);
+    else gemv2_launch_nb<TYPE, 5>(a, lg, maxrows, ch, st);
+    return true;
+}
+
 template <int TYPE, int LG, int MAXB>
 static void gemv_launch_t(const GemvArgs &a, bool safe, hipStream_t st) {
     constexpr int rows_per_block = 4 * (64 / LG);
@@ -197,7 +604,7 @@ int launch_gemv(const DevMat *const *mats, const GemvIn *in, const GemvOut *out,
     memset(&a, 0, sizeof a);
     a.nop = nmat;
     a.batch = batch;
-    int total = 0, nbmax = 0;
+    int total = 0, nbmax = 0, maxrows = 0;
     bool safe = false;
     const uint32_t type = mats[0]->type;
     for (int i = 0; i < nmat; i++) {
@@ -221,17 +628,29 @@ int launch_gemv(const DevMat *const *mats, const GemvIn *in, const GemvOut *out,
         o.row_begin = total;
         total += m.rows;
         if (m.nb > nbmax) nbmax = m.nb;
+        if (m.rows > maxrows) maxrows = m.rows;
         if ((m.cols % 32) != 0 || (in[i].ldx % 4) != 0 || (((uintptr_t)in[i].x) & 15) != 0) safe = true;
     }
     a.total_rows = total;
+    bool done = false;
     switch (type) {
-    case 0: gemv_launch_type<0>(a, nbmax, safe, st); break;
-    case 2: gemv_launch_type<2>(a, nbmax, safe, st); break;
-    case 3: gemv_launch_type<3>(a, nbmax, safe, st); break;
-    case 6: gemv_launch_type<6>(a, nbmax, safe, st); break;
-    case 7: gemv_launch_type<7>(a, nbmax, safe, st); break;
-    case 8: gemv_launch_type<8>(a, nbmax, safe, st); break;
-    default: return fail(WH_ERR_UNSUPPORTED, "gemv: unsupported matrix type");
+    case 2: done = gemv2_launch<2>(a, maxrows, nbmax, st); break;
+    case 3: done = gemv2_launch<3>(a, maxrows, nbmax, st); break;
+    case 6: done = gemv2_launch<6>(a, maxrows, nbmax, st); break;
+    case 7: done = gemv2_launch<7>(a, maxrows, nbmax, st); break;
+    case 8: done = gemv2_launch<8>(a, maxrows, nbmax, st); break;
+    default: break;
+    }
+    if (!done) {
+        switch (type) {
+        case 0: gemv_launch_type<0>(a, nbmax, safe, st); break;
+        case 2: gemv_launch_type<2>(a, nbmax, safe, st); break;
+        case 3: gemv_launch_type<3>(a, nbmax, safe, st); break;
+        case 6: gemv_launch_type<6>(a, nbmax, safe, st); break;
+        case 7: gemv_launch_type<7>(a, nbmax, safe, st); break;
+        case 8: gemv_launch_type<8>(a, nbmax, safe, st); break;
+        default: return fail(WH_ERR_UNSUPPORTED, "gemv: unsupported matrix type");
+        }
     }
     WH_HIP(hipGetLastError());
     return WH_OK;
