@@ -257,7 +257,7 @@ def run_gemv(args):
     fmts = args.gemv_formats.split(",")
     st = wh.native.Stream()
     e0, e1 = wh.native.Event(), wh.native.Event()
-    hip = HipGraphs()
+    hip = None if args.gemv_single else HipGraphs()
     rows_out = []
     for fmt in fmts:
         qt = QNAMES[fmt]
@@ -281,18 +281,18 @@ def run_gemv(args):
                 # graph, timed per graph launch: the kernel plus the gap between
                 # kernels, not the rate at which Python can issue launches; median
                 nlaunch = max(64, ncopy)
-                graph = hip.capture(st.h, lambda: [lib.wh_gemv(mats[i % ncopy], x.ptr, batch, y.ptr, st.h)
-                                                   for i in range(nlaunch)])
                 times = []
-                for rep in range(12):
-                    e0.record(st)
-                    hip.launch(graph, st.h)
-                    e1.record(st)
-                    st.sync()
-                    if rep >= 2:
-                        times.append(e0.elapsed_ms(e1) / nlaunch)
-                hip.destroy(graph)
-                ms = float(np.median(times))
+                if not args.gemv_single:
+                    graph = hip.capture(st.h, lambda: [lib.wh_gemv(mats[i % ncopy], x.ptr, batch, y.ptr, st.h)
+                                                       for i in range(nlaunch)])
+                    for rep in range(12):
+                        e0.record(st)
+                        hip.launch(graph, st.h)
+                        e1.record(st)
+                        st.sync()
+                        if rep >= 2:
+                            times.append(e0.elapsed_ms(e1) / nlaunch)
+                    hip.destroy(graph)
                 # one launch alone between its own pair of events (includes the
                 # launch and event latency)
                 single = []
@@ -302,11 +302,13 @@ def run_gemv(args):
                     e1.record(st)
                     st.sync()
                     single.append(e0.elapsed_ms(e1))
+                ms = float(np.median(times if times else single))
                 gbs = nbytes / (ms * 1e-3) / 1e9
                 rows_out.append({"format": fmt, "rows": rows, "cols": cols, "batch": batch, "bytes": nbytes,
                                  "us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
                                  "us_single_launch": round(float(np.median(single)) * 1e3, 3),
-                                 "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": ncopy})
+                                 "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": ncopy,
+                                 "timing": "graph" if times else "single"})
                 log(json.dumps(rows_out[-1]))
             for h in mats:
                 lib.wh_matrix_destroy(h)
@@ -328,6 +330,9 @@ def main():
                     help="first copy this many MiB device to device (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--gemv", action="store_true", help="run the standalone GEMV microbench instead")
     ap.add_argument("--gemv-formats", default="Q8_0,Q4_0,Q4_1,Q5_0,Q5_1")
+    ap.add_argument("--gemv-single", action="store_true",
+                    help="GEMV microbench: single launches between event pairs only, no graph "
+                         "(for kernel-trace profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench: this build runs on one GPU; --gpus {args.gpus} is not supported "
