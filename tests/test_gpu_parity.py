@@ -59,9 +59,12 @@ def test_dequant_reference_kats(wh, gpu):
 
 
 @pytest.mark.parametrize("qtype", QTYPES + [0])
-@pytest.mark.parametrize("shape", [(64, 128), (1280, 1280), (96, 5120), (37, 100), (300, 384)])
-@pytest.mark.parametrize("batch", [1, 5, 16])
+@pytest.mark.parametrize("shape", [(64, 128), (1280, 1280), (96, 5120), (37, 100), (300, 384), (20, 50)])
+@pytest.mark.parametrize("batch", [1, 2, 3, 5, 16])
 def test_gemv_vs_oracle(wh, orc, gpu, qtype, shape, batch):
+    """Batch 1, 2 and 3..5 (the last two staged with zero rows) take the LDS-staged
+    kernels, 16 the register-sliced one; (96, 5120) at batch 5 stages x in column
+    chunks; (20, 50) has rows of x that are not 16-byte aligned."""
     rows, cols = shape
     rng = np.random.default_rng(rows * 7 + cols + qtype)
     w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
