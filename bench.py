@@ -16,6 +16,8 @@ Also reported:
   cores, one thread (the reference's batch-1 GEMV is single-threaded), on a
   bounded sample of the same workload.
 
+`--workload beam5|streams16` instead times one of the batched workloads (beam 5
+over the small decoder in Q5_1; 16 large-v3 Q4_1 streams) as one Decode call.
 `--gemv` instead runs the standalone quantised-GEMV microbench (rows x cols at
 batch 1 and 5 for each format, rotating over >= 1 GiB of distinct copies;
 back-to-back launches replayed from a HIP graph, time per launch).
@@ -195,6 +197,64 @@ def run_decode(args):
     print(json.dumps(out), flush=True)
 
 
+def run_batched(args):
+    """The two batched workloads: beam 5 over the small decoder in Q5_1 (128 steps)
+    and 16 independent large-v3 Q4_1 streams with prompts of 4..224 tokens (128
+    greedy tokens each). Each is one Decode call (decode_tokens, decode_batch) timed
+    end to end, cross K/V precompute and host bookkeeping included; a short call of
+    the same kind runs first, untimed."""
+    wh = __graft_entry__.load_package()
+    if wh.native.device_count() < 1:
+        raise SystemExit("bench: no GPU visible")
+    prompt0 = list(wh.synth.SOT_EN_TRANSCRIBE)
+    if args.workload == "beam5":
+        config, qname, beam, n_tok = "small", "Q5_1", 5, 128
+        tensors, meta = wh.synth.make_decoder(config, QNAMES[qname])
+        d = meta["n_state"]
+        enc = wh.synth.encoder_output(config, d, stream=0)
+        dec = wh.HIPDecoder(tensors, meta, device=0)
+        dec.decode_tokens(enc, wh.DecoderParams(prompt=prompt0, beam_size=beam, max_tokens=4, no_fallback=True))
+        p = wh.DecoderParams(prompt=prompt0, beam_size=beam, max_tokens=n_tok, no_fallback=True)
+        t1 = time.perf_counter()
+        toks = dec.decode_tokens(enc, p)
+        dt = time.perf_counter() - t1
+        steps = len(toks) - len(prompt0)
+        wbytes = wh.synth.weight_bytes_per_token(tensors)
+        out = {"metric": "beam-5 decode steps/s (small Q5_1)", "value": round(steps / dt, 2), "unit": "steps/s",
+               "n_gpus": 1, "steps": steps, "higher_is_better": True, "ms_per_step": round(dt * 1e3 / max(steps, 1), 4),
+               "hypothesis_tokens_per_s": round(beam * steps / dt, 2), "dtype": "f32", "data": "synthetic",
+               "weight_bytes_per_step": wbytes,
+               "weight_roofline_frac": round(wbytes * steps / dt / (HBM_PEAK_GBS * 1e9), 4),
+               "config": {"workload": f"whisper {config} decoder, {qname} weights, beam {beam}, {n_tok} tokens, "
+                                      f"1500x{d} synthetic encoder output, one Decode call", "global_batch": beam}}
+    else:
+        config, qname, S, n_tok = "large-v3", "Q4_1", 16, 128
+        tensors, meta = wh.synth.make_decoder(config, QNAMES[qname])
+        d = meta["n_state"]
+        encs = [wh.synth.encoder_output(config, d, stream=i) for i in range(S)]
+        rng = np.random.default_rng(16)
+        lens = rng.integers(4, 225, size=S)
+        vocab_ids = rng.integers(0, 50000, size=(S, 224))
+        prompts = [prompt0 + [int(t) for t in vocab_ids[i, :lens[i] - len(prompt0)]] for i in range(S)]
+        dec = wh.HIPDecoder(tensors, meta, device=0)
+        dec.decode_batch(encs[:2], [wh.DecoderParams(prompt=prompts[i], max_tokens=4, no_fallback=True)
+                                    for i in range(2)])
+        params = [wh.DecoderParams(prompt=prompts[i], max_tokens=n_tok, no_fallback=True) for i in range(S)]
+        t1 = time.perf_counter()
+        got = dec.decode_batch(encs, params)
+        dt = time.perf_counter() - t1
+        gen = sum(len(g) - len(prompts[i]) for i, g in enumerate(got))
+        out = {"metric": "16-stream batched decode tokens/s (large-v3 Q4_1)", "value": round(gen / dt, 2),
+               "unit": "tokens/s", "n_gpus": 1, "higher_is_better": True, "tokens": gen,
+               "ms_per_step": round(dt * 1e3 / n_tok, 4), "dtype": "f32", "data": "synthetic",
+               "config": {"workload": f"whisper {config} decoder, {qname} weights, {S} streams, prompts "
+                                      f"{int(lens.min())}..{int(lens.max())} tokens, {n_tok} greedy tokens each, "
+                                      f"1500x{d} synthetic encoder outputs, one batched Decode call",
+                          "global_batch": S}}
+    dec.close()
+    print(json.dumps(out), flush=True)
+
+
 class HipGraphs:
     """Stream capture into a HIP graph through the HIP runtime the library
     already loaded (the microbench's launch loop, replayed without Python)."""
@@ -329,6 +389,8 @@ def main():
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="first copy this many MiB device to device (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--gemv", action="store_true", help="run the standalone GEMV microbench instead")
+    ap.add_argument("--workload", choices=["beam5", "streams16"], default=None,
+                    help="run one of the batched workloads instead (beam 5 small Q5_1; 16 large-v3 Q4_1 streams)")
     ap.add_argument("--gemv-formats", default="Q8_0,Q4_0,Q4_1,Q5_0,Q5_1")
     ap.add_argument("--gemv-single", action="store_true",
                     help="GEMV microbench: single launches between event pairs only, no graph "
@@ -340,6 +402,8 @@ def main():
         sys.exit(2)
     if args.gemv:
         run_gemv(args)
+    elif args.workload:
+        run_batched(args)
     else:
         run_decode(args)
 

@@ -213,3 +213,29 @@ def test_textbook_attention_mode_runs(wh, orc, gpu):
     s2.set_tokens(0, [1])
     _, m0 = s2.step_greedy(logits=True)
     assert rel_err(l0[0], m0[0]) < 1e-6
+
+
+@pytest.mark.parametrize("temperature", [1.0, 0.7])
+def test_step_topk_vs_oracle(wh, orc, gpu, temperature):
+    """Per-row top-k and log-probabilities (decoder.go:1068-1136) on the device
+    against the oracle's top-k of the same raw logits after the oracle's
+    repetition penalty: a 51864-entry vocabulary, split over 26 partitions on the
+    device, two streams with different histories."""
+    tensors, meta = _model(wh, "topk", 8, (51864, 64, 2, 1, 32))
+    encs = [wh.synth.encoder_output("topk", 64, stream=i, enc_len=40) for i in range(2)]
+    dec = wh.HIPDecoder(tensors, meta)
+    seq = dec.sequence(encs)
+    prompts = [[50258, 50259, 50359], [11, 11, 503, 4096, 11]]
+    for i, p in enumerate(prompts):
+        seq.set_tokens(i, p)
+    k = 6
+    tok, lp, logits = seq.step_topk(k=k, temperature=temperature, logits=True)
+    for i, p in enumerate(prompts):
+        pen = orc.repetition_penalty(logits[i], np.array(p, np.int32))
+        want_tok, want_lp = orc.topk(pen, k, temperature)
+        assert tok[i].tolist() == want_tok.tolist(), i
+        logz = float(np.log(np.sum(np.exp((pen / temperature).astype(np.float64) - np.max(pen / temperature))))) \
+            + float(np.max(pen / temperature))
+        assert np.max(np.abs(lp[i] - want_lp)) < 1e-5 * max(1.0, abs(logz)), (lp[i], want_lp)
+    seq.close()
+    dec.close()

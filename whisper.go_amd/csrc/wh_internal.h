@@ -160,7 +160,9 @@ int launch_beam_select(const int32_t *ttok, const float *tlp, int k, int kk, con
                        const int32_t *len_in, int32_t *hist_out, int32_t *len_out, int cap, float *score,
                        int32_t *nbeams, int32_t *active, int32_t *tok, int32_t *pos, int32_t *stop,
                        const float *powtab, int bs, int eot, hipStream_t st);
+// top-k scratch: TOPK_ROWS_MAX x TOPK_PARTS partitions x (2 + 2 * 8) floats
+constexpr int TOPK_ROWS_MAX = 16, TOPK_PARTS = 32, TOPK_SCRATCH_FLOATS = TOPK_ROWS_MAX * TOPK_PARTS * 18;
 int launch_topk(const float *cur, const int32_t *active, int S, int V, int k, float inv_temp, int32_t *out_tok,
-                float *out_lp, float *out_logz, hipStream_t st);
+                float *out_lp, float *out_logz, float *part, hipStream_t st);
 
 }  // namespace wh

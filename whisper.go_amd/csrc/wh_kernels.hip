@@ -546,10 +546,13 @@ static void gemv2_launch_nb(const GemvArgs &a, int lg, int maxrows, int ch, hipS
 }
 
 // Quantised GEMV with x staged in LDS: batch 1 (x up to 64 * GEMV2_KB blocks) and
-// batches 2..5; anything else is not handled here (k_gemv takes it).
+// batches 2..5 of matrices with at least 1024 rows; anything else is not handled
+// here (k_gemv takes it). Below 1024 rows the batched kernel stages five rows of x
+// per workgroup for a few weight rows and k_gemv is faster (768x768 at batch 5:
+// 6.7 against 10.2 us; 1280x1280: equal; 5120x1280: 22 against 13 us).
 template <int TYPE>
 static bool gemv2_launch(const GemvArgs &a, int maxrows, int nbmax, hipStream_t st) {
-    if (nbmax > 64 * GEMV2_KB || a.batch > 5) return false;
+    if (nbmax > 64 * GEMV2_KB || a.batch > 5 || (a.batch > 1 && maxrows < 1024)) return false;
     if (a.batch == 1) {
         switch (gemv2_lanes(nbmax, a.total_rows, 1)) {
         case 4: gemv1_launch_t<TYPE, 4>(a, maxrows, nbmax, st); break;
@@ -1311,86 +1314,144 @@ int launch_argmax_final(const SampleBufs &b, const float *cur, int S, int V, int
 constexpr int TOPK_MAX = 8;
 constexpr int BEAM_MAX = 16;
 
-__global__ __launch_bounds__(256) void k_topk(const float *cur, const int32_t *active, int V, int k, float inv_temp,
-                                              int32_t *out_tok, float *out_lp, float *out_logz) {
-    __shared__ float cv[256 * TOPK_MAX];
-    __shared__ int ci[256 * TOPK_MAX];
-    __shared__ float red[8];
-    __shared__ float selv[TOPK_MAX];
-    __shared__ int seli[TOPK_MAX];
-    __shared__ int wi[4], ws[4];
-    const int s = blockIdx.x;
+// Top-k of each row of cur * inv_temp by (value desc, index asc), with
+// logZ = log(sum_i exp(x_i - max)) + max (each exp in float64, summed in float32).
+// Three launches over P partitions of each row (grid P x S): k_topk_part keeps each
+// partition's max and its top-k (every entry of the row's top-k is in its
+// partition's top-k), k_topk_sum adds the partition's exp terms against the row's
+// max, and k_topk_merge picks the row's top-k from the P * k candidates and forms
+// logZ. Scratch per (row, partition): TOPK_PART floats (max, sum, k values, k
+// indices).
+constexpr int TOPK_PART = 2 + 2 * TOPK_MAX;
+
+__device__ __forceinline__ bool topk_before(float v, int i, float w, int j) { return v > w || (v == w && i < j); }
+
+// Block-wide: the best (value desc, index asc) over one candidate per thread, k
+// rounds; the chosen are written to outv/outi[0..k) in order. Candidates already
+// chosen are masked by index. All 256 threads call it.
+__device__ void topk_block_select(float v, int i, int k, float *outv, int *outi, float *redv, int *redi) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int r = 0; r < k; r++) {
+        float bv = v;
+        int bi = i;
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (oi != 0x7FFFFFFF && (bi == 0x7FFFFFFF || topk_before(ov, oi, bv, bi))) { bv = ov; bi = oi; }
+        }
+        if (lane == 0) { redv[wave] = bv; redi[wave] = bi; }
+        __syncthreads();
+        float b0 = redv[0];
+        int i0 = redi[0];
+        for (int w = 1; w < 4; w++)
+            if (redi[w] != 0x7FFFFFFF && (i0 == 0x7FFFFFFF || topk_before(redv[w], redi[w], b0, i0))) { b0 = redv[w]; i0 = redi[w]; }
+        if (threadIdx.x == 0) { outv[r] = b0; outi[r] = i0; }
+        if (i == i0) i = 0x7FFFFFFF;  // indices are distinct: only the chosen one drops out
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(256) void k_topk_part(const float *cur, const int32_t *active, int V, int k,
+                                                   float inv_temp, int P, float *part) {
+    __shared__ float redv[4], selv[TOPK_MAX];
+    __shared__ int redi[4], seli[TOPK_MAX];
+    const int s = blockIdx.y, p = blockIdx.x;
     if (active && !active[s]) return;
     const float *x = cur + (size_t)s * V;
+    const int chunk = (V + P - 1) / P, lo = p * chunk, hi = min(V, lo + chunk);
+    // this thread's top TOPK_MAX (constant indices: registers), then the max
     float tv[TOPK_MAX];
     int ti[TOPK_MAX];
+#pragma unroll
     for (int j = 0; j < TOPK_MAX; j++) { tv[j] = -INFINITY; ti[j] = 0x7FFFFFFF; }
     float mx = -INFINITY;
-    for (int i = threadIdx.x; i < V; i += blockDim.x) {
-        float v = x[i] * inv_temp;
+    for (int i = lo + threadIdx.x; i < hi; i += 256) {
+        const float v = x[i] * inv_temp;
         mx = fmaxf(mx, v);
-        // insert into the local sorted list (value desc, index asc)
-        if (v > tv[k - 1] || (v == tv[k - 1] && i < ti[k - 1])) {
-            int j = k - 1;
-            while (j > 0 && (v > tv[j - 1] || (v == tv[j - 1] && i < ti[j - 1]))) {
-                tv[j] = tv[j - 1]; ti[j] = ti[j - 1]; j--;
+        if (ti[TOPK_MAX - 1] == 0x7FFFFFFF || topk_before(v, i, tv[TOPK_MAX - 1], ti[TOPK_MAX - 1])) {
+            tv[TOPK_MAX - 1] = v;
+            ti[TOPK_MAX - 1] = i;
+#pragma unroll
+            for (int j = TOPK_MAX - 1; j > 0; j--) {
+                if (ti[j - 1] == 0x7FFFFFFF || topk_before(tv[j], ti[j], tv[j - 1], ti[j - 1])) {
+                    const float fv = tv[j]; tv[j] = tv[j - 1]; tv[j - 1] = fv;
+                    const int fi = ti[j]; ti[j] = ti[j - 1]; ti[j - 1] = fi;
+                }
             }
-            tv[j] = v; ti[j] = i;
         }
     }
-    for (int j = 0; j < k; j++) { cv[threadIdx.x * TOPK_MAX + j] = tv[j]; ci[threadIdx.x * TOPK_MAX + j] = ti[j]; }
-    // global max
     mx = group_max<64>(mx);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) red[wave] = mx;
+    if (lane == 0) redv[wave] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    mx = fmaxf(fmaxf(redv[0], redv[1]), fmaxf(redv[2], redv[3]));
     __syncthreads();
-    float es = 0.0f;
-    for (int i = threadIdx.x; i < V; i += blockDim.x) es += (float)exp((double)(x[i] * inv_temp - mx));
-    float sum = block_sum256(es, red);
-    const float logz = (float)log((double)sum) + mx;
-    // k rounds of block-wide selection over the 256*k candidates
+    // the partition's top k: k rounds, each thread offering the best of its own list
+    // not yet taken (its list is in order, so that is its next entry)
+    int head = 0;
+    float *o = part + ((size_t)s * P + p) * TOPK_PART;
     for (int r = 0; r < k; r++) {
-        float bv = -INFINITY;
-        int bi = 0x7FFFFFFF, bslot = -1;
-        for (int j = 0; j < k; j++) {
-            int slot = threadIdx.x * TOPK_MAX + j;
-            float v = cv[slot];
-            int i = ci[slot];
-            if (i != 0x7FFFFFFF && (v > bv || (v == bv && i < bi))) { bv = v; bi = i; bslot = slot; }
-        }
-        for (int o = 32; o > 0; o >>= 1) {
-            float ov = __shfl_xor(bv, o, 64);
-            int oi = __shfl_xor(bi, o, 64);
-            int os = __shfl_xor(bslot, o, 64);
-            if (oi != 0x7FFFFFFF && (ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; bslot = os; }
-        }
-        __syncthreads();
-        if (lane == 0) { red[wave] = bv; wi[wave] = bi; ws[wave] = bslot; }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            float b0 = red[0];
-            int i0 = wi[0], s0 = ws[0];
-            for (int w = 1; w < 4; w++)
-                if (wi[w] != 0x7FFFFFFF && (red[w] > b0 || (red[w] == b0 && wi[w] < i0))) { b0 = red[w]; i0 = wi[w]; s0 = ws[w]; }
-            selv[r] = b0;
-            seli[r] = i0;
-            if (s0 >= 0) ci[s0] = 0x7FFFFFFF;
-        }
+        float v = -INFINITY;
+        int i = 0x7FFFFFFF;
+#pragma unroll
+        for (int j = 0; j < TOPK_MAX; j++)
+            if (j == head) { v = tv[j]; i = ti[j]; }
+        topk_block_select(v, i, 1, selv + r, seli + r, redv, redi);
+        if (i != 0x7FFFFFFF && i == seli[r]) head++;
         __syncthreads();
     }
+    if (threadIdx.x == 0) o[0] = mx;
+    if (threadIdx.x < k) {
+        o[2 + threadIdx.x] = selv[threadIdx.x];
+        o[2 + TOPK_MAX + threadIdx.x] = __int_as_float(seli[threadIdx.x]);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_topk_sum(const float *cur, const int32_t *active, int V, float inv_temp,
+                                                  int P, float *part) {
+    __shared__ float red[8];
+    const int s = blockIdx.y, p = blockIdx.x;
+    if (active && !active[s]) return;
+    const float *x = cur + (size_t)s * V;
+    float mx = -INFINITY;
+    for (int q = 0; q < P; q++) mx = fmaxf(mx, part[((size_t)s * P + q) * TOPK_PART]);
+    const int chunk = (V + P - 1) / P, lo = p * chunk, hi = min(V, lo + chunk);
+    float es = 0.0f;
+    for (int i = lo + threadIdx.x; i < hi; i += 256) es += (float)exp((double)(x[i] * inv_temp - mx));
+    const float sum = block_sum256(es, red);
+    if (threadIdx.x == 0) part[((size_t)s * P + p) * TOPK_PART + 1] = sum;
+}
+
+__global__ __launch_bounds__(256) void k_topk_merge(const int32_t *active, int k, int P, const float *part,
+                                                    int32_t *out_tok, float *out_lp, float *out_logz) {
+    __shared__ float redv[4], selv[TOPK_MAX];
+    __shared__ int redi[4], seli[TOPK_MAX];
+    const int s = blockIdx.x;
+    if (active && !active[s]) return;
+    const float *ps = part + (size_t)s * P * TOPK_PART;
+    // candidate t = (partition t / k, place t % k); P * k <= 256
+    const int t = threadIdx.x;
+    float v = -INFINITY;
+    int i = 0x7FFFFFFF;
+    if (t < P * k) {
+        v = ps[(t / k) * TOPK_PART + 2 + t % k];
+        i = __float_as_int(ps[(t / k) * TOPK_PART + 2 + TOPK_MAX + t % k]);
+    }
+    topk_block_select(v, i, k, selv, seli, redv, redi);
+    if (threadIdx.x == 0) {
+        float mx = -INFINITY, sum = 0.0f;
+        for (int q = 0; q < P; q++) mx = fmaxf(mx, ps[q * TOPK_PART]);
+        for (int q = 0; q < P; q++) sum += ps[q * TOPK_PART + 1];
+        redv[0] = (float)log((double)sum) + mx;
+    }
+    __syncthreads();
+    const float logz = redv[0];
     if (threadIdx.x < k) {
         out_tok[(size_t)s * k + threadIdx.x] = seli[threadIdx.x];
         out_lp[(size_t)s * k + threadIdx.x] = selv[threadIdx.x] - logz;
     }
     if (threadIdx.x == 0) out_logz[s] = logz;
 }
-
-// ---------------------------------------------------------------------------
-// Beam-search bookkeeping on the device (internal/model/decoder.go:528-726):
-// the candidates, their order and the next hypotheses never leave the GPU.
-// ---------------------------------------------------------------------------
 
 // Rows of k_topk ([S][kk], kk = k + 1) with equal values at or inside the k-th
 // place: the kept set and its order are those of the reference's streaming
@@ -1565,9 +1626,14 @@ int launch_beam_select(const int32_t *ttok, const float *tlp, int k, int kk, con
 }
 
 int launch_topk(const float *cur, const int32_t *active, int S, int V, int k, float inv_temp, int32_t *out_tok,
-                float *out_lp, float *out_logz, hipStream_t st) {
+                float *out_lp, float *out_logz, float *part, hipStream_t st) {
     if (k < 1 || k > TOPK_MAX) return fail(WH_ERR_INVALID, "topk: k must be in [1,8]");
-    hipLaunchKernelGGL(k_topk, dim3(S), dim3(256), 0, st, cur, active, V, k, inv_temp, out_tok, out_lp, out_logz);
+    if (S < 1 || S > TOPK_ROWS_MAX) return fail(WH_ERR_INVALID, "topk: 1..16 rows");
+    // partitions of ~2048 entries, at most TOPK_PARTS (P * k <= 256 candidates to merge)
+    const int P = std::max(1, std::min(TOPK_PARTS, (V + 2047) / 2048));
+    hipLaunchKernelGGL(k_topk_part, dim3(P, S), dim3(256), 0, st, cur, active, V, k, inv_temp, P, part);
+    hipLaunchKernelGGL(k_topk_sum, dim3(P, S), dim3(256), 0, st, cur, active, V, inv_temp, P, part);
+    hipLaunchKernelGGL(k_topk_merge, dim3(S), dim3(256), 0, st, active, k, P, part, out_tok, out_lp, out_logz);
     WH_HIP(hipGetLastError());
     return WH_OK;
 }

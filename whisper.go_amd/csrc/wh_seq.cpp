@@ -40,7 +40,7 @@ struct wh_seq {
     wh::SampleBufs sb{};
     int32_t *hist = nullptr, *hist_len = nullptr, *tok = nullptr, *pos = nullptr, *active = nullptr;
     int32_t *out_ids = nullptr, *topk_tok = nullptr;
-    float *topk_lp = nullptr, *topk_logz = nullptr;
+    float *topk_lp = nullptr, *topk_logz = nullptr, *topk_part = nullptr;
     std::vector<int32_t> h_len;     // host mirror of hist_len
     std::vector<int32_t> h_active;  // host mirror of active
     std::vector<std::vector<int32_t>> h_hist;  // host mirror of the histories
@@ -526,6 +526,7 @@ int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t e
     ALLOC(s->topk_tok, (size_t)S * 8);
     ALLOC(s->topk_lp, (size_t)S * 8);
     ALLOC(s->topk_logz, (size_t)S);
+    ALLOC(s->topk_part, (size_t)TOPK_SCRATCH_FLOATS);
 #undef ALLOC
     WH_HIP(hipMemsetAsync(s->hist_len, 0, sizeof(int32_t) * S, s->st));
     WH_HIP(hipMemsetAsync(s->tok, 0, sizeof(int32_t) * S, s->st));
@@ -713,7 +714,7 @@ int seq_step_topk(wh_seq *s, const int32_t *active, int32_t k, float temperature
         return rc;
     // one extra candidate exposes a tie at the k-th place
     const int kk = std::min(k + 1, 8);
-    if ((rc = launch_topk(s->sb.cur, s->active, s->S, V, kk, inv, s->topk_tok, s->topk_lp, s->topk_logz, s->st)))
+    if ((rc = launch_topk(s->sb.cur, s->active, s->S, V, kk, inv, s->topk_tok, s->topk_lp, s->topk_logz, s->topk_part, s->st)))
         return rc;
     int32_t *h_tok = s->pinned_ids;
     float *h_lp = (float *)(s->pinned_ids + 16 * 8);
@@ -977,7 +978,7 @@ int decode_beam(const wh_model *m, const float *enc, int32_t enc_len, int32_t en
         WH_HIP(hipGetLastError());
         if ((rc = seq_forward(q)) ||
             (rc = launch_penalty_argmax(q.logits, q.hist, q.hist_len, hc, q.active, bs, V, inv, eot, q.sb, q.st)) ||
-            (rc = launch_topk(q.sb.cur, q.active, bs, V, KK, inv, q.topk_tok, q.topk_lp, q.topk_logz, q.st)) ||
+            (rc = launch_topk(q.sb.cur, q.active, bs, V, KK, inv, q.topk_tok, q.topk_lp, q.topk_logz, q.topk_part, q.st)) ||
             (rc = launch_topk_ties(q.sb.cur, q.active, bs, V, K, KK, inv, q.topk_logz, q.topk_tok, q.topk_lp, q.st)) ||
             (rc = launch_beam_select(q.topk_tok, q.topk_lp, K, KK, q.hist, q.hist_len, hist_alt, len_alt, hc, score,
                                      nbeams, q.active, q.tok, q.pos, stop, powtab, bs, eot, q.st)))
