@@ -507,6 +507,176 @@ __global__ __launch_bounds__(256) void k_gemv2(GemvArgs a, int ch) {
     }
 }
 
+// ---- batches up to 16 on the matrix cores ----
+// D (16 batch rows x 16 weight rows) += A (16 x 4: x) x B (4 x 16: codes) with
+// v_mfma_f32_16x16x4f32: fp32 operands (the codes are small exact integers), fp32
+// accumulation. Lane l: batch row / weight row l % 16, k slot kq = l / 16; the j-th
+// of a block's 8 products covers columns 4j .. 4j + 3, so the lane takes element
+// 4j + kq of its x row and of its weight row; D register i of lane l is batch row
+// 4 kq + i, weight row l % 16. Each block's 8 products go to a fresh tile that is
+// scaled (d, and the offset or m through the block sums of x) into the total. A
+// workgroup takes 16 weight rows; its four waves take the blocks in turn and their
+// tiles are summed through LDS at the end. x is staged per chunk of CH blocks as
+// [block][kq][batch row][j] (two float4 reads per lane per block), rows past the
+// batch as zeros: CH = 20 (42 KiB of LDS), or 40 (84 KiB, one workgroup per CU)
+// for matrices of at most 2048 rows, whose grid is below the CU count anyway and
+// whose time goes to staging rounds (1280x5120 at batch 16: 8 rounds of 20 blocks).
+#ifndef GEMVM_MIN_BATCH
+#define GEMVM_MIN_BATCH 6
+#endif
+
+typedef float gemvm_f4 __attribute__((ext_vector_type(4)));
+
+// element 4j + kq (j = 0..7) of a raw block as a float code (signed for Q8_0)
+template <int TYPE>
+__device__ __forceinline__ void mfma_codes(const RawBlk &r, int kq, float (&q)[8]) {
+    if constexpr (TYPE == 8) {
+        const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+        for (int j = 0; j < 8; j++) q[j] = (float)(int)__builtin_amdgcn_sbfe((int)w[j], 8 * kq, 8);  // the builtin's type is unsigned
+    } else {
+        const uint32_t w[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+        // element e = 4j + kq: byte 2j + kq / 2, nibble kq & 1
+        const int sh0 = 8 * (kq >> 1) + 4 * (kq & 1);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            uint32_t c = (w[j >> 1] >> (16 * (j & 1) + sh0)) & 0xFu;
+            if constexpr (TYPE == 6 || TYPE == 7) c |= ((r.h >> (4 * j + kq)) & 1u) << 4;
+            q[j] = (float)c;
+        }
+    }
+}
+
+template <int TYPE, int CH>
+__global__ __launch_bounds__(256) void k_gemv_mfma(GemvArgs a) {
+    constexpr int NBW = CH / 4;  // blocks per wave per chunk
+    extern __shared__ float xm[];  // CH * 512 floats of x, then CH * 16 block sums
+    const GemvOpDev &op = a.op[blockIdx.y];
+    const int nb = op.nb, batch = a.batch;
+    const int r0 = blockIdx.x * 16;
+    if (r0 >= op.rows) return;  // the whole workgroup: past this op's rows
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lr = lane & 15, kq = lane >> 4;
+    const int row = min(r0 + lr, op.rows - 1);  // past the last row: re-read it, drop it
+    float *sxs = xm + CH * 512;
+    const bool vec = (((uintptr_t)op.x) & 15) == 0 && (op.ldx & 3) == 0 && (op.cols & 3) == 0;
+    gemvm_f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int cb = 0; cb < nb; cb += CH) {
+        const int nbc = min(CH, nb - cb);
+        // this wave's blocks of the chunk (cb + wave + 4u): raw loads first
+        RawBlk rb[NBW];
+#pragma unroll
+        for (int u = 0; u < NBW; u++)
+            if (wave + 4 * u < nbc) raw_load<TYPE>(op, (size_t)row * nb + cb + wave + 4 * u, rb[u]);
+        // x: 16 batch rows x nbc blocks x 8 float4 (columns 4j .. 4j + 3 of a block)
+        const int nall = 16 * nbc * 8;
+        if (vec) {
+            for (int i0 = 0; i0 < nall; i0 += 256 * 4) {
+                float4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int i = i0 + 256 * u + tid, b = i / (nbc * 8), f = i - b * (nbc * 8);
+                    const int e = 32 * (cb + (f >> 3)) + 4 * (f & 7);
+                    v[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    if (i < nall && b < batch && e < op.cols) v[u] = *(const float4 *)(op.x + (size_t)b * op.ldx + e);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int i = i0 + 256 * u + tid, b = i / (nbc * 8), f = i - b * (nbc * 8);
+                    if (i < nall) {
+                        float *o = xm + (((f >> 3) * 4) * 16 + b) * 8 + (f & 7);  // kq = 0
+                        o[0] = v[u].x; o[128] = v[u].y; o[256] = v[u].z; o[384] = v[u].w;
+                    }
+                }
+            }
+        } else {
+            for (int i = tid; i < 4 * nall; i += 256) {
+                const int q4 = i >> 2, b = q4 / (nbc * 8), f = q4 - b * (nbc * 8), k = i & 3;
+                const int e = 32 * (cb + (f >> 3)) + 4 * (f & 7) + k;
+                xm[(((f >> 3) * 4 + k) * 16 + b) * 8 + (f & 7)] =
+                    (b < batch && e < op.cols) ? op.x[(size_t)b * op.ldx + e] : 0.0f;
+            }
+        }
+        __syncthreads();
+        if constexpr (TYPE != 8) {
+            for (int i = tid; i < 16 * nbc; i += 256) {
+                const int bl = i >> 4, b = i & 15;
+                float sum = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const float4 *p = (const float4 *)(xm + ((bl * 4 + k) * 16 + b) * 8);
+                    const float4 p0 = p[0], p1 = p[1];
+                    sum += ((p0.x + p0.y) + (p0.z + p0.w)) + ((p1.x + p1.y) + (p1.z + p1.w));
+                }
+                sxs[bl * 16 + b] = sum;
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int u = 0; u < NBW; u++) {
+            const int bl = wave + 4 * u;
+            if (bl < nbc) {
+                const float4 *xp = (const float4 *)(xm + ((bl * 4 + kq) * 16 + lr) * 8);
+                const float4 x0 = xp[0], x1 = xp[1];
+                float q[8];
+                mfma_codes<TYPE>(rb[u], kq, q);
+                gemvm_f4 t = {0.0f, 0.0f, 0.0f, 0.0f};
+                t = __builtin_amdgcn_mfma_f32_16x16x4f32(x0.x, q[0], t, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x4f32(x0.y, q[1], t, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x4f32(x0.z, q[2], t, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x4f32(x0.w, q[3], t, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x4f32(x1.x, q[4], t, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x4f32(x1.y, q[5], t, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x4f32(x1.z, q[6], t, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x4f32(x1.w, q[7], t, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float sx = TYPE == 8 ? 0.0f : sxs[bl * 16 + 4 * kq + i];
+                    acc[i] += block_scale<TYPE>(rb[u], t[i], sx);
+                }
+            }
+        }
+        __syncthreads();  // x and the sums are restaged (or reused for the tiles below)
+    }
+    // the four waves' tiles
+    gemvm_f4 *red = (gemvm_f4 *)xm;
+    red[wave * 64 + lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+        gemvm_f4 sum = red[lane];
+#pragma unroll
+        for (int w = 1; w < 4; w++) sum += red[w * 64 + lane];
+        const int r = r0 + lr;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int b = 4 * kq + i;
+            if (b < batch && r < op.rows) {
+                float v = sum[i];
+                if (op.bias) v = v + op.bias[r];
+                if (op.gelu) v = gelu_ref(v);
+                if (op.res) v = op.res[(size_t)b * op.ldres + r] + v;
+                op.y[(size_t)b * op.ldy + r] = v;
+            }
+        }
+    }
+}
+
+template <int TYPE>
+static bool gemvm_launch(const GemvArgs &a, int maxrows, hipStream_t st) {
+    if (a.batch < GEMVM_MIN_BATCH || a.batch > 16) return false;
+    const dim3 grid((maxrows + 15) / 16, a.nop);
+    constexpr size_t lds40 = (size_t)40 * (512 + 16) * 4;
+    // the dynamic LDS above the default 64 KiB, asked once; refused: 20-block chunks
+    static const bool big = hipFuncSetAttribute((const void *)k_gemv_mfma<TYPE, 40>,
+                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds40) == hipSuccess;
+    if (maxrows <= 2048 && big) {
+        hipLaunchKernelGGL((k_gemv_mfma<TYPE, 40>), grid, dim3(256), lds40, st, a);
+    } else {
+        hipLaunchKernelGGL((k_gemv_mfma<TYPE, 20>), grid, dim3(256), (size_t)20 * (512 + 16) * 4, st, a);
+    }
+    return true;
+}
+
 constexpr int GEMV2_LDS = 64 * 1024;
 
 // Lanes per row: the fewest (a power of two, at least 4) whose GEMV2_KB blocks each
@@ -637,11 +807,11 @@ int launch_gemv(const DevMat *const *mats, const GemvIn *in, const GemvOut *out,
     a.total_rows = total;
     bool done = false;
     switch (type) {
-    case 2: done = gemv2_launch<2>(a, maxrows, nbmax, st); break;
-    case 3: done = gemv2_launch<3>(a, maxrows, nbmax, st); break;
-    case 6: done = gemv2_launch<6>(a, maxrows, nbmax, st); break;
-    case 7: done = gemv2_launch<7>(a, maxrows, nbmax, st); break;
-    case 8: done = gemv2_launch<8>(a, maxrows, nbmax, st); break;
+    case 2: done = gemv2_launch<2>(a, maxrows, nbmax, st) || gemvm_launch<2>(a, maxrows, st); break;
+    case 3: done = gemv2_launch<3>(a, maxrows, nbmax, st) || gemvm_launch<3>(a, maxrows, st); break;
+    case 6: done = gemv2_launch<6>(a, maxrows, nbmax, st) || gemvm_launch<6>(a, maxrows, st); break;
+    case 7: done = gemv2_launch<7>(a, maxrows, nbmax, st) || gemvm_launch<7>(a, maxrows, st); break;
+    case 8: done = gemv2_launch<8>(a, maxrows, nbmax, st) || gemvm_launch<8>(a, maxrows, st); break;
     default: break;
     }
     if (!done) {
