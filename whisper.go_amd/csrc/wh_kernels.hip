@@ -515,14 +515,18 @@ __global__ __launch_bounds__(256) void k_gemv2(GemvArgs a, int ch) {
 // 4j + kq of its x row and of its weight row; D register i of lane l is batch row
 // 4 kq + i, weight row l % 16. Each block's 8 products go to a fresh tile that is
 // scaled (d, and the offset or m through the block sums of x) into the total. A
-// workgroup takes 16 weight rows; its four waves take the blocks in turn and their
-// tiles are summed through LDS at the end. x is staged per chunk of CH blocks as
+// workgroup takes 16 weight rows; its NW waves take the blocks in turn and their
+// tiles are summed through LDS at the end (NW = 4, or 16 for matrices of at most
+// 2048 rows, whose 16-row workgroups are too few to fill the chip). x is staged per chunk of CH blocks as
 // [block][kq][batch row][j] (two float4 reads per lane per block), rows past the
 // batch as zeros: CH = 20 (42 KiB of LDS), or 40 (84 KiB, one workgroup per CU)
 // for matrices of at most 2048 rows, whose grid is below the CU count anyway and
 // whose time goes to staging rounds (1280x5120 at batch 16: 8 rounds of 20 blocks).
 #ifndef GEMVM_MIN_BATCH
 #define GEMVM_MIN_BATCH 6
+#endif
+#ifndef GEMVM_NW_SMALL
+#define GEMVM_NW_SMALL 16  // waves per workgroup for matrices of at most 2048 rows
 #endif
 
 typedef float gemvm_f4 __attribute__((ext_vector_type(4)));
@@ -547,9 +551,9 @@ __device__ __forceinline__ void mfma_codes(const RawBlk &r, int kq, float (&q)[8
     }
 }
 
-template <int TYPE, int CH>
-__global__ __launch_bounds__(256) void k_gemv_mfma(GemvArgs a) {
-    constexpr int NBW = CH / 4;  // blocks per wave per chunk
+template <int TYPE, int CH, int NW>
+__global__ __launch_bounds__(64 * NW) void k_gemv_mfma(GemvArgs a) {
+    constexpr int NT = 64 * NW, NBW = (CH + NW - 1) / NW;  // threads; blocks per wave per chunk
     extern __shared__ float xm[];  // CH * 512 floats of x, then CH * 16 block sums
     const GemvOpDev &op = a.op[blockIdx.y];
     const int nb = op.nb, batch = a.batch;
@@ -563,26 +567,26 @@ __global__ __launch_bounds__(256) void k_gemv_mfma(GemvArgs a) {
     gemvm_f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int cb = 0; cb < nb; cb += CH) {
         const int nbc = min(CH, nb - cb);
-        // this wave's blocks of the chunk (cb + wave + 4u): raw loads first
+        // this wave's blocks of the chunk (cb + wave + NW u): raw loads first
         RawBlk rb[NBW];
 #pragma unroll
         for (int u = 0; u < NBW; u++)
-            if (wave + 4 * u < nbc) raw_load<TYPE>(op, (size_t)row * nb + cb + wave + 4 * u, rb[u]);
+            if (wave + NW * u < nbc) raw_load<TYPE>(op, (size_t)row * nb + cb + wave + NW * u, rb[u]);
         // x: 16 batch rows x nbc blocks x 8 float4 (columns 4j .. 4j + 3 of a block)
         const int nall = 16 * nbc * 8;
         if (vec) {
-            for (int i0 = 0; i0 < nall; i0 += 256 * 4) {
+            for (int i0 = 0; i0 < nall; i0 += NT * 4) {
                 float4 v[4];
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
-                    const int i = i0 + 256 * u + tid, b = i / (nbc * 8), f = i - b * (nbc * 8);
+                    const int i = i0 + NT * u + tid, b = i / (nbc * 8), f = i - b * (nbc * 8);
                     const int e = 32 * (cb + (f >> 3)) + 4 * (f & 7);
                     v[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                     if (i < nall && b < batch && e < op.cols) v[u] = *(const float4 *)(op.x + (size_t)b * op.ldx + e);
                 }
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
-                    const int i = i0 + 256 * u + tid, b = i / (nbc * 8), f = i - b * (nbc * 8);
+                    const int i = i0 + NT * u + tid, b = i / (nbc * 8), f = i - b * (nbc * 8);
                     if (i < nall) {
                         float *o = xm + (((f >> 3) * 4) * 16 + b) * 8 + (f & 7);  // kq = 0
                         o[0] = v[u].x; o[128] = v[u].y; o[256] = v[u].z; o[384] = v[u].w;
@@ -590,7 +594,7 @@ __global__ __launch_bounds__(256) void k_gemv_mfma(GemvArgs a) {
                 }
             }
         } else {
-            for (int i = tid; i < 4 * nall; i += 256) {
+            for (int i = tid; i < 4 * nall; i += NT) {
                 const int q4 = i >> 2, b = q4 / (nbc * 8), f = q4 - b * (nbc * 8), k = i & 3;
                 const int e = 32 * (cb + (f >> 3)) + 4 * (f & 7) + k;
                 xm[(((f >> 3) * 4 + k) * 16 + b) * 8 + (f & 7)] =
@@ -599,7 +603,7 @@ __global__ __launch_bounds__(256) void k_gemv_mfma(GemvArgs a) {
         }
         __syncthreads();
         if constexpr (TYPE != 8) {
-            for (int i = tid; i < 16 * nbc; i += 256) {
+            for (int i = tid; i < 16 * nbc; i += NT) {
                 const int bl = i >> 4, b = i & 15;
                 float sum = 0.0f;
 #pragma unroll
@@ -614,7 +618,7 @@ __global__ __launch_bounds__(256) void k_gemv_mfma(GemvArgs a) {
         }
 #pragma unroll
         for (int u = 0; u < NBW; u++) {
-            const int bl = wave + 4 * u;
+            const int bl = wave + NW * u;
             if (bl < nbc) {
                 const float4 *xp = (const float4 *)(xm + ((bl * 4 + kq) * 16 + lr) * 8);
                 const float4 x0 = xp[0], x1 = xp[1];
@@ -638,14 +642,14 @@ __global__ __launch_bounds__(256) void k_gemv_mfma(GemvArgs a) {
         }
         __syncthreads();  // x and the sums are restaged (or reused for the tiles below)
     }
-    // the four waves' tiles
+    // the waves' tiles (NW KiB of LDS)
     gemvm_f4 *red = (gemvm_f4 *)xm;
     red[wave * 64 + lane] = acc;
     __syncthreads();
     if (wave == 0) {
         gemvm_f4 sum = red[lane];
 #pragma unroll
-        for (int w = 1; w < 4; w++) sum += red[w * 64 + lane];
+        for (int w = 1; w < NW; w++) sum += red[w * 64 + lane];
         const int r = r0 + lr;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -667,12 +671,12 @@ static bool gemvm_launch(const GemvArgs &a, int maxrows, hipStream_t st) {
     const dim3 grid((maxrows + 15) / 16, a.nop);
     constexpr size_t lds40 = (size_t)40 * (512 + 16) * 4;
     // the dynamic LDS above the default 64 KiB, asked once; refused: 20-block chunks
-    static const bool big = hipFuncSetAttribute((const void *)k_gemv_mfma<TYPE, 40>,
+    static const bool big = hipFuncSetAttribute((const void *)k_gemv_mfma<TYPE, 40, GEMVM_NW_SMALL>,
                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds40) == hipSuccess;
     if (maxrows <= 2048 && big) {
-        hipLaunchKernelGGL((k_gemv_mfma<TYPE, 40>), grid, dim3(256), lds40, st, a);
+        hipLaunchKernelGGL((k_gemv_mfma<TYPE, 40, GEMVM_NW_SMALL>), grid, dim3(64 * GEMVM_NW_SMALL), lds40, st, a);
     } else {
-        hipLaunchKernelGGL((k_gemv_mfma<TYPE, 20>), grid, dim3(256), (size_t)20 * (512 + 16) * 4, st, a);
+        hipLaunchKernelGGL((k_gemv_mfma<TYPE, 20, 4>), grid, dim3(256), (size_t)20 * (512 + 16) * 4, st, a);
     }
     return true;
 }
