@@ -1627,11 +1627,11 @@ __global__ __launch_bounds__(256) void k_topk_merge(const int32_t *active, int k
     if (threadIdx.x == 0) out_logz[s] = logz;
 }
 
-// Rows of k_topk ([S][kk], kk = k + 1) with equal values at or inside the k-th
+// Rows of the top-k ([S][kk], kk = k + 1) with equal values at or inside the k-th
 // place: the kept set and its order are those of the reference's streaming
 // replace-min scan (decoder.go:1089-1121) followed by a stable sort by value
 // (decoder.go:1123-1127), so one thread reruns that scan over the penalised row
-// and rewrites the first k entries. Other rows keep k_topk's (value desc, index
+// and rewrites the first k entries. Other rows keep the top-k's (value desc, index
 // asc) result, which is the same when no values tie.
 __global__ __launch_bounds__(64) void k_topk_ties(const float *cur, const int32_t *active, int V, int k, int kk,
                                                   float inv_temp, const float *logz, int32_t *tok, float *lp) {

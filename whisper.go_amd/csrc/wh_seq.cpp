@@ -908,7 +908,7 @@ int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, 
 // decoder.go:528-726. The beam_size hypotheses run as one batch; every
 // hypothesis is reset before its forward (P9), the cross K/V are shared and
 // computed once (the reference recomputes identical values each step). The
-// bookkeeping runs on the device: top-k with log-normaliser (k_topk, plus the
+// bookkeeping runs on the device: top-k with log-normaliser (launch_topk, plus the
 // reference's scan for rows with ties), candidate ranking by normalised score
 // (a stable order among exact ties where Go's sort.Slice is unstable), the
 // prune and the next hypotheses' histories (k_beam_select). The host reads one
