@@ -60,11 +60,12 @@ def test_dequant_reference_kats(wh, gpu):
 
 @pytest.mark.parametrize("qtype", QTYPES + [0])
 @pytest.mark.parametrize("shape", [(64, 128), (1280, 1280), (96, 5120), (37, 100), (300, 384), (20, 50)])
-@pytest.mark.parametrize("batch", [1, 2, 3, 5, 16])
+@pytest.mark.parametrize("batch", [1, 2, 3, 5, 7, 16])
 def test_gemv_vs_oracle(wh, orc, gpu, qtype, shape, batch):
     """Batch 1, 2 and 3..5 (the last two staged with zero rows) take the LDS-staged
-    kernels, 16 the register-sliced one; (96, 5120) at batch 5 stages x in column
-    chunks; (20, 50) has rows of x that are not 16-byte aligned."""
+    kernels on matrices of >= 1024 rows and the register-sliced one below; 7 and 16
+    the matrix-core kernel (7 with zero rows); (96, 5120) stages x in column chunks;
+    (20, 50) has rows of x that are not 16-byte aligned."""
     rows, cols = shape
     rng = np.random.default_rng(rows * 7 + cols + qtype)
     w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
@@ -166,6 +167,19 @@ def test_beam_tied_logits(wh, orc, gpu):
     got = dec.decode_tokens(enc, p)
     assert got == ref.decode(enc, p)
     assert len(got) > 3
+
+
+def test_batch_of_seven_streams(wh, orc, gpu):
+    """Seven streams (the matrix-core GEMV at batch 7, ragged prompts) against the
+    oracle's single-stream decode of each."""
+    tensors, meta = _model(wh, "batch7", 7, (1200, 128, 2, 2, 64))
+    dec = wh.HIPDecoder(tensors, meta)
+    ref = orc.OracleModel(tensors, meta)
+    encs = [wh.synth.encoder_output("batch7", 128, stream=i, enc_len=60) for i in range(7)]
+    params = [wh.DecoderParams(prompt=list(range(3, 4 + 2 * i)), max_tokens=10, no_fallback=True) for i in range(7)]
+    got = dec.decode_batch(encs, params)
+    for i in range(7):
+        assert got[i] == ref.decode(encs[i], params[i]), i
 
 
 def test_batch_equals_single_streams(wh, orc, gpu):
