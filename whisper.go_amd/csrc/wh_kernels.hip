@@ -490,19 +490,28 @@ __global__ __launch_bounds__(256) void k_gemv2(GemvArgs a, int ch) {
         }
         if (cb + ch < nb) __syncthreads();  // the next chunk overwrites x
     }
+    // every lane of a group holds every sum after the butterfly; the group's lanes
+    // share the RW * NB outputs (one lane doing them all serialised ten float64 tanh
+    // evaluations of the GELU)
+    constexpr int NO = RW * NB;
+    float sums[NO];
 #pragma unroll
-    for (int u = 0; u < RW; u++) {
+    for (int u = 0; u < RW; u++)
 #pragma unroll
-        for (int m = 0; m < NB; m++) {
-            const float s = group_sum<LG>(acc[u][m]);
-            const int rr = row + u;
-            if (m < batch && gl == 0 && rr < op.rows) {
-                float v = s;
-                if (op.bias) v = v + op.bias[rr];
-                if (op.gelu) v = gelu_ref(v);
-                if (op.res) v = op.res[(size_t)m * op.ldres + rr] + v;
-                op.y[(size_t)m * op.ldy + rr] = v;
-            }
+        for (int m = 0; m < NB; m++) sums[u * NB + m] = group_sum<LG>(acc[u][m]);
+#pragma unroll
+    for (int p0 = 0; p0 < NO; p0 += LG) {
+        const int p = p0 + gl;
+        float v = 0.0f;
+#pragma unroll
+        for (int q = 0; q < NO; q++)
+            if (q == p) v = sums[q];
+        const int u = p / NB, m = p - u * NB, rr = row + u;
+        if (p < NO && m < batch && rr < op.rows) {
+            if (op.bias) v = v + op.bias[rr];
+            if (op.gelu) v = gelu_ref(v);
+            if (op.res) v = op.res[(size_t)m * op.ldres + rr] + v;
+            op.y[(size_t)m * op.ldy + rr] = v;
         }
     }
 }
@@ -642,25 +651,28 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_mfma(GemvArgs a) {
         }
         __syncthreads();  // x and the sums are restaged (or reused for the tiles below)
     }
-    // the waves' tiles (NW KiB of LDS)
+    // the waves' tiles (NW KiB of LDS), summed in wave order; then one output per
+    // thread of the first 256 (batch row t / 16, weight row t % 16) for the epilogue
     gemvm_f4 *red = (gemvm_f4 *)xm;
+    float *outs = xm + NW * 64 * 4;
     red[wave * 64 + lane] = acc;
     __syncthreads();
     if (wave == 0) {
         gemvm_f4 sum = red[lane];
 #pragma unroll
         for (int w = 1; w < NW; w++) sum += red[w * 64 + lane];
-        const int r = r0 + lr;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int b = 4 * kq + i;
-            if (b < batch && r < op.rows) {
-                float v = sum[i];
-                if (op.bias) v = v + op.bias[r];
-                if (op.gelu) v = gelu_ref(v);
-                if (op.res) v = op.res[(size_t)b * op.ldres + r] + v;
-                op.y[(size_t)b * op.ldy + r] = v;
-            }
+        for (int i = 0; i < 4; i++) outs[(4 * kq + i) * 16 + lr] = sum[i];
+    }
+    __syncthreads();
+    if (tid < 256) {
+        const int b = tid >> 4, r = r0 + (tid & 15);
+        if (b < batch && r < op.rows) {
+            float v = outs[tid];
+            if (op.bias) v = v + op.bias[r];
+            if (op.gelu) v = gelu_ref(v);
+            if (op.res) v = op.res[(size_t)b * op.ldres + r] + v;
+            op.y[(size_t)b * op.ldy + r] = v;
         }
     }
 }
