@@ -169,14 +169,9 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Batch-1 quantised GEMV, the streaming form: a wave owns rows in a grid-stride
-// loop and each lane always handles the same blocks (g, g+LG, ... of its group's
-// row), so its 32-element slices of x are loaded into registers once per matrix
-// and reused for every row. The raw blocks of U rows are loaded before any of
-// them is decoded, which keeps U rows of blocks in flight per wave; the
-// codes are converted exactly and s = sum q_i x_i is accumulated in fp32, scaled
-// once by d (plus m * sum x for the _1 formats), as the batched kernel above.
-// LG lanes per row (64/LG rows per wave step), KB = ceil(nb / LG) blocks per lane.
+// Raw blocks for the LDS-staged GEMVs below: a lane loads a block's code bytes,
+// scale word(s) and Q5 high bits as they sit in the device layout (16-byte loads
+// for the codes) and decodes them where it multiplies.
 // ---------------------------------------------------------------------------
 struct RawBlk {
     uint4 a, b;  // 32 code bytes (Q8_0), or 16 (a) for the 4/5-bit formats
