@@ -933,11 +933,43 @@ __device__ __forceinline__ float block_sum256(float v, float *red) {
     return t;
 }
 
+constexpr int LN_KEEP = 8;  // values of x a thread keeps in registers (rows up to 2048)
+
 __global__ __launch_bounds__(256) void k_layernorm(const float *x, const float *w, const float *b, float *y,
                                                    int d) {
     __shared__ float red[8];
     const float *xr = x + (size_t)blockIdx.x * d;
     float *yr = y + (size_t)blockIdx.x * d;
+    if (d <= 256 * LN_KEEP) {
+        // the row read once: a thread keeps its values (elements t, t + 256, ...) for
+        // the three passes, in the same order and arithmetic as below
+        float xv[LN_KEEP];
+#pragma unroll
+        for (int j = 0; j < LN_KEEP; j++) {
+            const int i = threadIdx.x + 256 * j;
+            xv[j] = i < d ? xr[i] : 0.0f;
+        }
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < LN_KEEP; j++)
+            if (threadIdx.x + 256 * j < d) s += xv[j];
+        const float mean = block_sum256(s, red) / (float)d;
+        float v = 0.0f;
+#pragma unroll
+        for (int j = 0; j < LN_KEEP; j++)
+            if (threadIdx.x + 256 * j < d) {
+                const float t = xv[j] - mean;
+                v += t * t;
+            }
+        const float var = block_sum256(v, red) / (float)d;
+        const float sd = (float)sqrt((double)(var + 1e-5f));
+#pragma unroll
+        for (int j = 0; j < LN_KEEP; j++) {
+            const int i = threadIdx.x + 256 * j;
+            if (i < d) yr[i] = w[i] * (xv[j] - mean) / sd + b[i];
+        }
+        return;
+    }
     float s = 0.0f;
     for (int i = threadIdx.x; i < d; i += blockDim.x) s += xr[i];
     float mean = block_sum256(s, red) / (float)d;
