@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstring>
 
@@ -677,10 +678,22 @@ static bool gemvm_launch(const GemvArgs &a, int maxrows, hipStream_t st) {
     if (a.batch < GEMVM_MIN_BATCH || a.batch > 16) return false;
     const dim3 grid((maxrows + 15) / 16, a.nop);
     constexpr size_t lds40 = (size_t)40 * (512 + 16) * 4;
-    // the dynamic LDS above the default 64 KiB, asked once; refused: 20-block chunks
-    static const bool big = hipFuncSetAttribute((const void *)k_gemv_mfma<TYPE, 40, GEMVM_NW_SMALL>,
-                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds40) == hipSuccess;
-    if (maxrows <= 2048 && big) {
+    // the dynamic LDS above the default 64 KiB, asked once per device (bit d of
+    // `granted`); refused: 20-block chunks
+    static std::atomic<uint32_t> granted{0};
+    bool big = false;
+    if (maxrows <= 2048) {
+        int dev = 0;
+        if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 32) {
+            big = (granted.load() >> dev) & 1u;
+            if (!big && hipFuncSetAttribute((const void *)k_gemv_mfma<TYPE, 40, GEMVM_NW_SMALL>,
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds40) == hipSuccess) {
+                granted.fetch_or(1u << dev);
+                big = true;
+            }
+        }
+    }
+    if (big) {
         hipLaunchKernelGGL((k_gemv_mfma<TYPE, 40, GEMVM_NW_SMALL>), grid, dim3(64 * GEMVM_NW_SMALL), lds40, st, a);
     } else {
         hipLaunchKernelGGL((k_gemv_mfma<TYPE, 20, 4>), grid, dim3(256), (size_t)20 * (512 + 16) * 4, st, a);
