@@ -1246,45 +1246,73 @@ int launch_cross_attn(const float *q, const float *const *kbase, const float *co
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // Weights 8g .. 8g+7 of block b of row r, dequantised exactly as dequant_elem.
+// The raw bytes behind elements 8g .. 8g+7 of block b of row r, and their
+// bit-exact conversion (split so a loop can load the next tile's raw bytes while it
+// works on the current one).
+struct Raw8 {
+    float4 x, y;       // F32
+    uint32_t w0, w1;   // code bytes (Q8_0: 8, the 4/5-bit formats: 4 in w0)
+    uint32_t sc, hb;   // scale word(s), Q5 high bits of these 8 elements
+};
+
 template <int TYPE>
-__device__ __forceinline__ void dequant8(const MatView &m, int r, int b, int g, float (&o)[8]) {
-#pragma clang fp contract(off)
+__device__ __forceinline__ void dq8_load(const MatView &m, int r, int b, int g, Raw8 &q) {
     const size_t blk = (size_t)r * m.nb + b;
     if constexpr (TYPE == 0) {
         const float4 *p = (const float4 *)((const float *)m.qs + blk * 32 + 8 * g);
-        const float4 x = p[0], y = p[1];
-        o[0] = x.x; o[1] = x.y; o[2] = x.z; o[3] = x.w; o[4] = y.x; o[5] = y.y; o[6] = y.z; o[7] = y.w;
+        q.x = p[0];
+        q.y = p[1];
     } else if constexpr (TYPE == 8) {
-        const float d = h2f(((const uint16_t *)m.sc)[blk]);
-        const uint2 q = *(const uint2 *)(m.qs + blk * 32 + 8 * g);
+        q.sc = ((const uint16_t *)m.sc)[blk];
+        const uint2 c = *(const uint2 *)(m.qs + blk * 32 + 8 * g);
+        q.w0 = c.x;
+        q.w1 = c.y;
+    } else {
+        q.w0 = *(const uint32_t *)(m.qs + blk * 16 + 4 * g);  // weights 8g .. 8g+7
+        if constexpr (TYPE == 3 || TYPE == 7) q.sc = ((const uint32_t *)m.sc)[blk];
+        else q.sc = ((const uint16_t *)m.sc)[blk];
+        if constexpr (TYPE == 6 || TYPE == 7) q.hb = (m.qh[blk] >> (8 * g)) & 0xFFu;
+    }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void dq8_convert(const Raw8 &q, float (&o)[8]) {
+#pragma clang fp contract(off)
+    if constexpr (TYPE == 0) {
+        o[0] = q.x.x; o[1] = q.x.y; o[2] = q.x.z; o[3] = q.x.w; o[4] = q.y.x; o[5] = q.y.y; o[6] = q.y.z; o[7] = q.y.w;
+    } else if constexpr (TYPE == 8) {
+        const float d = h2f(q.sc);
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const uint32_t w = j < 4 ? q.x : q.y;
+            const uint32_t w = j < 4 ? q.w0 : q.w1;
             o[j] = d * (float)(int)(int8_t)(w >> (8 * (j & 3)));
         }
     } else {
-        const uint32_t bytes = *(const uint32_t *)(m.qs + blk * 16 + 4 * g);  // weights 8g .. 8g+7
-        uint32_t hb = 0;
-        if constexpr (TYPE == 6 || TYPE == 7) hb = (m.qh[blk] >> (8 * g)) & 0xFFu;
         float d, mn = 0.0f;
         if constexpr (TYPE == 3 || TYPE == 7) {
-            const uint32_t w = ((const uint32_t *)m.sc)[blk];
-            d = h2f(w & 0xFFFFu);
-            mn = h2f(w >> 16);
+            d = h2f(q.sc & 0xFFFFu);
+            mn = h2f(q.sc >> 16);
         } else {
-            d = h2f(((const uint16_t *)m.sc)[blk]);
+            d = h2f(q.sc);
         }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const uint32_t byte = (bytes >> (8 * (j >> 1))) & 0xFFu;
+            const uint32_t byte = (q.w0 >> (8 * (j >> 1))) & 0xFFu;
             uint32_t nib = (j & 1) ? (byte >> 4) : (byte & 0xFu);
-            if constexpr (TYPE == 6 || TYPE == 7) nib |= ((hb >> j) & 1u) << 4;
+            if constexpr (TYPE == 6 || TYPE == 7) nib |= ((q.hb >> j) & 1u) << 4;
             if constexpr (TYPE == 2) o[j] = d * (float)((int32_t)nib - 8);
             else if constexpr (TYPE == 3) o[j] = mul_add_nofma(d, (float)nib, mn);
             else if constexpr (TYPE == 6) o[j] = d * (float)((int32_t)nib - 16);
             else o[j] = mul_add_nofma(d, (float)nib, mn);
         }
     }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void dequant8(const MatView &m, int r, int b, int g, float (&o)[8]) {
+    Raw8 q;
+    dq8_load<TYPE>(m, r, b, g, q);
+    dq8_convert<TYPE>(q, o);
 }
 
 template <int TYPE>
@@ -1297,23 +1325,29 @@ __global__ __launch_bounds__(256) void k_cross_gemm(MatView w, const float *E, i
     const int K = w.cols;
     const int lr = tid >> 2, lg = tid & 3;  // tile loads: row (frame) lr, elements 8 lg .. 8 lg + 7
     f32x16 acc = {};
+    // the next K tile in registers: its loads are in flight while the current tile's
+    // products run
+    float4 ex = make_float4(0.f, 0.f, 0.f, 0.f), ey = ex;
+    Raw8 wq = {};
+    auto load_tile = [&](int b) {
+        const int t = t0 + lr;
+        ex = make_float4(0.f, 0.f, 0.f, 0.f);
+        ey = ex;
+        if (t < T) {
+            const float4 *p = (const float4 *)(E + (size_t)t * K + b * 32 + 8 * lg);
+            ex = p[0];
+            ey = p[1];
+        }
+        if (r0 + lr < w.rows) dq8_load<TYPE>(w, r0 + lr, b, lg, wq);
+    };
+    load_tile(0);
     for (int b = 0; b < w.nb; b++) {
         {
-            const int t = t0 + lr;
-            float4 x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
-            if (t < T) {
-                const float4 *p = (const float4 *)(E + (size_t)t * K + b * 32 + 8 * lg);
-                x = p[0];
-                y = p[1];
-            }
             float *e = &Es[lr][8 * lg];
-            e[0] = x.x; e[1] = x.y; e[2] = x.z; e[3] = x.w; e[4] = y.x; e[5] = y.y; e[6] = y.z; e[7] = y.w;
-        }
-        {
-            const int r = r0 + lr;
+            e[0] = ex.x; e[1] = ex.y; e[2] = ex.z; e[3] = ex.w; e[4] = ey.x; e[5] = ey.y; e[6] = ey.z; e[7] = ey.w;
             float o[8];
-            if (r < w.rows) {
-                dequant8<TYPE>(w, r, b, lg, o);
+            if (r0 + lr < w.rows) {
+                dq8_convert<TYPE>(wq, o);
             } else {
 #pragma unroll
                 for (int j = 0; j < 8; j++) o[j] = 0.0f;
@@ -1322,6 +1356,7 @@ __global__ __launch_bounds__(256) void k_cross_gemm(MatView w, const float *E, i
             for (int j = 0; j < 8; j++) Ws[lr][8 * lg + j] = o[j];
         }
         __syncthreads();
+        if (b + 1 < w.nb) load_tile(b + 1);
         // A (32 frames x 2 k): lane -> frame lane % 32, k lane / 32; B (2 k x 32 rows) likewise
 #pragma unroll
         for (int kk = 0; kk < 32; kk += 2) {
