@@ -232,10 +232,8 @@ def run_batched(args):
         tensors, meta = wh.synth.make_decoder(config, QNAMES[qname])
         d = meta["n_state"]
         encs = [wh.synth.encoder_output(config, d, stream=i) for i in range(S)]
-        rng = np.random.default_rng(16)
-        lens = rng.integers(4, 225, size=S)
-        vocab_ids = rng.integers(0, 50000, size=(S, 224))
-        prompts = [prompt0 + [int(t) for t in vocab_ids[i, :lens[i] - len(prompt0)]] for i in range(S)]
+        prompts = wh.synth.stream_prompts(S)
+        lens = np.array([len(p) for p in prompts])
         dec = wh.HIPDecoder(tensors, meta, device=0)
         dec.decode_batch(encs[:2], [wh.DecoderParams(prompt=prompts[i], max_tokens=4, no_fallback=True)
                                     for i in range(2)])

@@ -511,6 +511,29 @@ static void *gemv_worker(void *p) {
     return NULL;
 }
 
+/* One input row, output rows [m0, m1) of the matrix: the same dot per output
+ * element as the serial loop, so the result does not depend on the split. Used
+ * only to generate test fixtures faster (the reference's batch-1 GEMV is serial,
+ * internal/ml/matmul_q8.go:110-118). */
+static void *gemv_rows_worker(void *p) {
+    gemv_job *j = (gemv_job *)p;
+    for (int r = j->m0; r < j->m1; r++)
+        j->out[r] = or_dot(j->type, j->w + (size_t)r * j->row_bytes, j->a, j->cols, j->variant);
+    return NULL;
+}
+
+static void gemv1_split(uint32_t type, const uint8_t *w, int rows, int cols, const float *a, float *out, int variant,
+                        int threads) {
+    size_t rb = or_row_bytes(type, (size_t)cols);
+    if (threads > 64) threads = 64;
+    gemv_job jobs[64];
+    pthread_t th[64];
+    for (int t = 0; t < threads; t++)
+        jobs[t] = (gemv_job){type, w, rows, cols, a, out, (t * rows) / threads, ((t + 1) * rows) / threads, variant, rb};
+    for (int t = 0; t < threads; t++) pthread_create(&th[t], NULL, gemv_rows_worker, &jobs[t]);
+    for (int t = 0; t < threads; t++) pthread_join(th[t], NULL);
+}
+
 int or_gemv(uint32_t type, const uint8_t *w, int rows, int cols, const float *a, int m, float *out,
             int variant, int threads) {
     size_t rb = or_row_bytes(type, (size_t)cols);
@@ -744,6 +767,7 @@ struct or_model {
     int n_vocab, n_state, n_head, n_layer, n_ctx;
     int32_t eot;
     int dot_variant, threads, fast_exp;
+    int fwd_threads; /* > 1: split the forward's GEMV rows over threads (fixture generation only) */
     omat tok; /* type!=0: tokenEmbQ (row lookups dequantize, the documented extension of P4) */
     float *pos;
     float *lnw, *lnb;
@@ -992,6 +1016,7 @@ void or_model_hparams(const or_model *m, int32_t *o) {
 }
 void or_model_set_eot(or_model *m, int32_t eot) { m->eot = eot; }
 void or_model_set_fast_exp(or_model *m, int on) { m->fast_exp = on; }
+void or_model_set_forward_threads(or_model *m, int n) { m->fwd_threads = n; }
 
 /* model/decoder.go:330-365 */
 or_state *or_state_create(const or_model *m, const int32_t *prompt, int plen) {
@@ -1047,6 +1072,11 @@ int or_state_push(or_state *s, int32_t tok) {
 }
 
 static void mat_gemv(const or_model *m, const omat *w, const float *a, int rows_a, float *out, int threads) {
+    if (rows_a == 1 && m->fwd_threads > 1 && (size_t)w->rows * w->cols >= (1u << 16)) {
+        gemv1_split(w->type, w->type == 0 ? (const uint8_t *)w->f : w->q, w->rows, w->cols, a, out, m->dot_variant,
+                    m->fwd_threads);
+        return;
+    }
     or_gemv(w->type, w->type == 0 ? (const uint8_t *)w->f : w->q, w->rows, w->cols, a, rows_a, out, m->dot_variant, threads);
 }
 
@@ -1168,26 +1198,196 @@ static int decode_greedy(const or_model *m, const float *enc, int enc_len, const
     return rc;
 }
 
-static void sort_cands(ocand *c, int n) { /* stable: documented tie-break for sort.Slice */
-    for (int i = 1; i < n; i++) {
-        ocand t = c[i]; int j = i - 1;
-        while (j >= 0 && c[j].norm < t.norm) { c[j + 1] = c[j]; j--; }
-        c[j + 1] = t;
+/* ---- Go's sort.Slice (third-party: the Go 1.25 standard library, src/sort/slice.go
+ * + zsortfunc.go, pattern-defeating quicksort "pdqsort_func"), restated for the
+ * beam candidates with the reference's less(i, j) = norm[i] > norm[j]
+ * (decoder.go:1462-1475). sort.Slice is not stable; the order it leaves equal
+ * candidates in decides which parent lands in which slot, so the algorithm is
+ * restated step by step: insertion sort up to 12 elements, median-of-three /
+ * Tukey-ninther pivots, partial insertion sort on presorted input, partition on
+ * duplicates, xorshift pattern breaking, heapsort fallback. */
+typedef struct { ocand *v; } gosort;
+static int gs_less(const gosort *d, int i, int j) { return d->v[i].norm > d->v[j].norm; }
+static void gs_swap(gosort *d, int i, int j) { ocand t = d->v[i]; d->v[i] = d->v[j]; d->v[j] = t; }
+static int go_bits_len(unsigned long x) { int n = 0; while (x) { n++; x >>= 1; } return n; }
+
+static void gs_insertion(gosort *d, int a, int b) {
+    for (int i = a + 1; i < b; i++)
+        for (int j = i; j > a && gs_less(d, j, j - 1); j--) gs_swap(d, j, j - 1);
+}
+static void gs_sift_down(gosort *d, int lo, int hi, int first) {
+    int root = lo;
+    for (;;) {
+        int child = 2 * root + 1;
+        if (child >= hi) return;
+        if (child + 1 < hi && gs_less(d, first + child, first + child + 1)) child++;
+        if (!gs_less(d, first + root, first + child)) return;
+        gs_swap(d, first + root, first + child);
+        root = child;
     }
 }
+static void gs_heapsort(gosort *d, int a, int b) {
+    int first = a, lo = 0, hi = b - a;
+    for (int i = (hi - 1) / 2; i >= 0; i--) gs_sift_down(d, i, hi, first);
+    for (int i = hi - 1; i >= 0; i--) { gs_swap(d, first, first + i); gs_sift_down(d, lo, i, first); }
+}
+static int gs_order2(gosort *d, int a, int b, int *swaps, int *lo) {
+    if (gs_less(d, b, a)) { (*swaps)++; *lo = b; return a; }
+    *lo = a; return b;
+}
+static int gs_median(gosort *d, int a, int b, int c, int *swaps) {
+    int x, y;
+    y = gs_order2(d, a, b, swaps, &x); a = x; b = y;
+    y = gs_order2(d, b, c, swaps, &x); b = x; c = y;
+    y = gs_order2(d, a, b, swaps, &x); a = x; b = y;
+    (void)c;
+    return b;
+}
+enum { GS_UNKNOWN = 0, GS_INCREASING = 1, GS_DECREASING = 2 };
+static int gs_choose_pivot(gosort *d, int a, int b, int *hint) {
+    const int l = b - a;
+    int swaps = 0, i = a + l / 4 * 1, j = a + l / 4 * 2, k = a + l / 4 * 3;
+    if (l >= 8) {
+        if (l >= 50) { /* Tukey ninther */
+            i = gs_median(d, i - 1, i, i + 1, &swaps);
+            j = gs_median(d, j - 1, j, j + 1, &swaps);
+            k = gs_median(d, k - 1, k, k + 1, &swaps);
+        }
+        j = gs_median(d, i, j, k, &swaps);
+    }
+    *hint = swaps == 0 ? GS_INCREASING : swaps == 12 ? GS_DECREASING : GS_UNKNOWN;
+    return j;
+}
+static void gs_reverse(gosort *d, int a, int b) {
+    for (int i = a, j = b - 1; i < j; i++, j--) gs_swap(d, i, j);
+}
+static int gs_partial_insertion(gosort *d, int a, int b) {
+    int i = a + 1;
+    for (int step = 0; step < 5; step++) {
+        while (i < b && !gs_less(d, i, i - 1)) i++;
+        if (i == b) return 1;
+        if (b - a < 50) return 0;
+        gs_swap(d, i, i - 1);
+        if (i - a >= 2)
+            for (int j = i - 1; j >= 1; j--) { if (!gs_less(d, j, j - 1)) break; gs_swap(d, j, j - 1); }
+        if (b - i >= 2)
+            for (int j = i + 1; j < b; j++) { if (!gs_less(d, j, j - 1)) break; gs_swap(d, j, j - 1); }
+    }
+    return 0;
+}
+static void gs_break_patterns(gosort *d, int a, int b) {
+    const int length = b - a;
+    if (length >= 8) {
+        uint64_t r = (uint64_t)length; /* xorshift seeded with the length */
+        const unsigned long modulus = 1ul << go_bits_len((unsigned long)length);
+        const int idx = a + (length / 4) * 2 - 1;
+        for (int i = 0; i < 3; i++) {
+            r ^= r << 13; r ^= r >> 7; r ^= r << 17;
+            int other = (int)((unsigned long)r & (modulus - 1));
+            if (other >= length) other -= length;
+            gs_swap(d, idx - 1 + i, a + other);
+        }
+    }
+}
+static int gs_partition_equal(gosort *d, int a, int b, int pivot) {
+    gs_swap(d, a, pivot);
+    int i = a + 1, j = b - 1;
+    for (;;) {
+        while (i <= j && !gs_less(d, a, i)) i++;
+        while (i <= j && gs_less(d, a, j)) j--;
+        if (i > j) break;
+        gs_swap(d, i, j); i++; j--;
+    }
+    return i;
+}
+static int gs_partition(gosort *d, int a, int b, int pivot, int *already) {
+    gs_swap(d, a, pivot);
+    int i = a + 1, j = b - 1;
+    while (i <= j && gs_less(d, i, a)) i++;
+    while (i <= j && !gs_less(d, j, a)) j--;
+    if (i > j) { gs_swap(d, j, a); *already = 1; return j; }
+    gs_swap(d, i, j); i++; j--;
+    for (;;) {
+        while (i <= j && gs_less(d, i, a)) i++;
+        while (i <= j && !gs_less(d, j, a)) j--;
+        if (i > j) break;
+        gs_swap(d, i, j); i++; j--;
+    }
+    gs_swap(d, j, a);
+    *already = 0;
+    return j;
+}
+static void gs_pdqsort(gosort *d, int a, int b, int limit) {
+    int was_balanced = 1, was_partitioned = 1;
+    for (;;) {
+        const int length = b - a;
+        if (length <= 12) { gs_insertion(d, a, b); return; }
+        if (limit == 0) { gs_heapsort(d, a, b); return; }
+        if (!was_balanced) { gs_break_patterns(d, a, b); limit--; }
+        int hint;
+        int pivot = gs_choose_pivot(d, a, b, &hint);
+        if (hint == GS_DECREASING) {
+            gs_reverse(d, a, b);
+            pivot = (b - 1) - (pivot - a);
+            hint = GS_INCREASING;
+        }
+        if (was_balanced && was_partitioned && hint == GS_INCREASING && gs_partial_insertion(d, a, b)) return;
+        if (a > 0 && !gs_less(d, a - 1, pivot)) { a = gs_partition_equal(d, a, b, pivot); continue; }
+        int already;
+        const int mid = gs_partition(d, a, b, pivot, &already);
+        was_partitioned = already;
+        const int left = mid - a, right = b - mid, thr = length / 8;
+        if (left < right) { was_balanced = left >= thr; gs_pdqsort(d, a, mid, limit); a = mid + 1; }
+        else { was_balanced = right >= thr; gs_pdqsort(d, mid + 1, b, limit); b = mid; }
+    }
+}
+/* sort.Slice(c, func(i, j) bool { return c[i].norm > c[j].norm }) */
+static void go_sort_cands(ocand *c, int n) {
+    gosort d = {c};
+    gs_pdqsort(&d, 0, n, go_bits_len((unsigned long)n));
+}
+void or_go_sort_norm(float *norm, int32_t *id, int n) {
+    ocand *c = (ocand *)calloc((size_t)(n > 0 ? n : 1), sizeof(ocand));
+    for (int i = 0; i < n; i++) { c[i].norm = norm[i]; c[i].parent = id[i]; }
+    go_sort_cands(c, n);
+    for (int i = 0; i < n; i++) { norm[i] = c[i].norm; id[i] = c[i].parent; }
+    free(c);
+}
 
-static int decode_beam(const or_model *m, const float *enc, int enc_len, const or_decode_params *p, int32_t *out,
-                       int cap, int32_t *out_len) {
+/* A Go `*beam` whose token slice has Go's length and capacity: make([]int32, n)
+ * has capacity n, reslicing within the capacity keeps the backing array
+ * (decoder.go:545-553, :636-658). Every beam owns its backing array. */
+typedef struct { int32_t *buf; int len, cap; float score; } gobeam;
+
+/* Beam search, decoder.go:528-726 (one attempt: no vocabulary, so no retry).
+ * The next hypotheses are built inside the beam objects of the current step,
+ * taken from the end of reusableBeams (:627-660): slot i reuses the object of
+ * beams[nbeams-1-i] while later candidates may still name it as their parent,
+ * so a parent is read as earlier slots left it; an object that is its own
+ * parent and must grow gets a fresh zeroed slice first, which is also what the
+ * copy then reads. Results for every beam object are exposed to tests through
+ * or_beam_run. */
+/* Per-step selection margins of the last beam_loop on this thread (test hook):
+ * the smallest gap between two different normalised scores among the first
+ * keep + 1 sorted candidates, i.e. how far the step's choice is from a reorder. */
+static __thread float *g_margin_out;
+static __thread int g_margin_cap;
+
+static int beam_loop(const or_model *m, const float *enc, int enc_len, const or_decode_params *p, gobeam **out_obj,
+                     int **out_order, int *out_nbeams, int *out_tcap) {
     float temp = p->temperature == 0 ? 1.0f : p->temperature;
     int bs = p->beam_size <= 0 ? 1 : p->beam_size;
     int mt = cap_max_tokens(m, p);
-    int tcap = p->prompt_len + mt + 2;
-    obeam *beams = (obeam *)calloc((size_t)bs, sizeof(obeam)), *next = (obeam *)calloc((size_t)bs, sizeof(obeam));
+    int tcap = p->prompt_len + bs * (mt + 1) + 2; /* a slot grows by at most one per earlier slot and step */
+    gobeam *obj = (gobeam *)calloc((size_t)bs, sizeof(gobeam));
+    int *order = (int *)malloc(sizeof(int) * (size_t)bs), *reuse = (int *)malloc(sizeof(int) * (size_t)bs);
+    int *next = (int *)malloc(sizeof(int) * (size_t)bs);
     for (int i = 0; i < bs; i++) {
-        beams[i].tokens = (int32_t *)malloc(sizeof(int32_t) * (size_t)tcap);
-        next[i].tokens = (int32_t *)malloc(sizeof(int32_t) * (size_t)tcap);
-        memcpy(beams[i].tokens, p->prompt, sizeof(int32_t) * (size_t)p->prompt_len);
-        beams[i].len = p->prompt_len; beams[i].score = 0;
+        obj[i].buf = (int32_t *)calloc((size_t)tcap, sizeof(int32_t));
+        memcpy(obj[i].buf, p->prompt, sizeof(int32_t) * (size_t)p->prompt_len);
+        obj[i].len = obj[i].cap = p->prompt_len;
+        obj[i].score = 0;
+        order[i] = i;
     }
     int nbeams = bs;
     or_state *s = or_state_create(m, p->prompt, p->prompt_len);
@@ -1196,62 +1396,124 @@ static int decode_beam(const or_model *m, const float *enc, int enc_len, const o
     ocand *cands = (ocand *)malloc(sizeof(ocand) * (size_t)bs * 6);
     int rc = 0;
     for (int step = 0; step < mt; step++) {
-        int nc = 0;
+        int nc = 0, nreuse = 0;
         for (int b = 0; b < nbeams; b++) {
-            obeam *h = &beams[b];
-            if (h->len > 0 && h->tokens[h->len - 1] == m->eot) {
+            gobeam *h = &obj[order[b]];
+            reuse[nreuse++] = order[b];
+            if (h->len > 0 && h->buf[h->len - 1] == m->eot) {
                 float norm = h->score / (float)pow((double)h->len, 0.6);
-                cands[nc++] = (ocand){b, h->score, m->eot, 0, norm};
+                cands[nc++] = (ocand){order[b], h->score, m->eot, 0, norm};
                 continue;
             }
-            or_state_reset(m, s, h->tokens, h->len);
+            or_state_reset(m, s, h->buf, h->len);
             if (or_forward(m, s, enc, enc_len, logits)) { rc = -1; goto done; }
-            or_repetition_penalty(logits, m->n_vocab, h->tokens, h->len, 2.0f, 128, cur);
+            or_repetition_penalty(logits, m->n_vocab, h->buf, h->len, 2.0f, 128, cur);
             int32_t tk[5]; float lp[5];
             int k = or_topk(cur, m->n_vocab, 5, temp, tk, lp);
             for (int c = 0; c < k; c++) {
                 int nl = h->len + 1;
                 float ns = h->score + lp[c];
                 float norm = ns / (float)pow((double)nl, 0.6);
-                cands[nc++] = (ocand){b, ns, tk[c], lp[c], norm};
+                cands[nc++] = (ocand){order[b], ns, tk[c], lp[c], norm};
             }
         }
-        sort_cands(cands, nc);
+        go_sort_cands(cands, nc);
         int keep = nc < bs ? nc : bs;
-        for (int i = 0; i < keep; i++) {
-            ocand *c = &cands[i];
-            obeam *par = &beams[c->parent];
-            obeam *nb = &next[i];
-            memcpy(nb->tokens, par->tokens, sizeof(int32_t) * (size_t)par->len);
-            nb->len = par->len;
-            int carry = par->len > 0 && par->tokens[par->len - 1] == m->eot && c->token == m->eot && c->logprob == 0;
-            if (!carry) nb->tokens[nb->len++] = c->token;
-            nb->score = c->score;
+        if (g_margin_out && step < g_margin_cap) {
+            float gap = INFINITY;
+            for (int i = 0; i < keep && i + 1 < nc; i++)
+                if (cands[i].norm != cands[i + 1].norm && cands[i].norm - cands[i + 1].norm < gap)
+                    gap = cands[i].norm - cands[i + 1].norm;
+            g_margin_out[step] = gap;
         }
-        obeam *tmp = beams; beams = next; next = tmp;
+        for (int i = 0; i < keep; i++) {
+            const ocand *c = &cands[i];
+            if (nreuse == 0) { set_err("oracle: beam object pool exhausted"); rc = -1; goto done; }
+            const int nbi = reuse[--nreuse];
+            gobeam *nb = &obj[nbi], *par = &obj[c->parent];
+            const int carry = par->len > 0 && par->buf[par->len - 1] == m->eot && c->token == m->eot && c->logprob == 0;
+            const int need = carry ? par->len : par->len + 1;
+            if (nb->cap < need) { /* nb.tokens = make([]int32, need) */
+                memset(nb->buf, 0, sizeof(int32_t) * (size_t)need);
+                nb->cap = need;
+            }
+            nb->len = need; /* or nb.tokens = nb.tokens[:need] */
+            if (nb != par) memcpy(nb->buf, par->buf, sizeof(int32_t) * (size_t)(carry ? need : need - 1));
+            if (!carry) nb->buf[need - 1] = c->token;
+            nb->score = c->score;
+            next[i] = nbi;
+        }
+        memcpy(order, next, sizeof(int) * (size_t)keep);
         nbeams = keep;
         int all_eot = 1;
-        for (int b = 0; b < nbeams; b++)
-            if (beams[b].len == 0 || beams[b].tokens[beams[b].len - 1] != m->eot) { all_eot = 0; break; }
+        for (int b = 0; b < nbeams; b++) {
+            const gobeam *h = &obj[order[b]];
+            if (h->len == 0 || h->buf[h->len - 1] != m->eot) { all_eot = 0; break; }
+        }
         if (all_eot) break;
-        if (nbeams > 0 && beams[0].len >= 2) {
-            int32_t last = beams[0].tokens[beams[0].len - 1];
+        if (nbeams > 0 && obj[order[0]].len >= 2) {
+            const gobeam *h = &obj[order[0]];
+            int32_t last = h->buf[h->len - 1];
             int streak = 1, stop = 0;
-            for (int i = beams[0].len - 2; i >= 0 && beams[0].tokens[i] == last; i--) {
+            for (int i = h->len - 2; i >= 0 && h->buf[i] == last; i--) {
                 streak++;
                 if (streak > 20) { stop = 1; break; }
             }
             if (stop) break;
         }
     }
-    if (nbeams == 0) *out_len = 0;
-    else if (beams[0].len > cap) { set_err("oracle: output capacity too small"); rc = -1; }
-    else { memcpy(out, beams[0].tokens, sizeof(int32_t) * (size_t)beams[0].len); *out_len = beams[0].len; }
 done:
     state_free_cross(m, s);
     or_state_destroy(s);
-    for (int i = 0; i < bs; i++) { free(beams[i].tokens); free(next[i].tokens); }
-    free(beams); free(next); free(logits); free(cur); free(cands);
+    free(logits); free(cur); free(cands); free(reuse); free(next);
+    *out_obj = obj; *out_order = order; *out_nbeams = nbeams; *out_tcap = tcap;
+    return rc;
+}
+
+static void beams_free(gobeam *obj, int *order, int bs) {
+    for (int i = 0; i < bs; i++) free(obj[i].buf);
+    free(obj); free(order);
+}
+
+static int decode_beam(const or_model *m, const float *enc, int enc_len, const or_decode_params *p, int32_t *out,
+                       int cap, int32_t *out_len) {
+    gobeam *obj; int *order, nbeams, tcap;
+    const int bs = p->beam_size <= 0 ? 1 : p->beam_size;
+    int rc = beam_loop(m, enc, enc_len, p, &obj, &order, &nbeams, &tcap);
+    if (rc == 0) {
+        if (nbeams == 0) *out_len = 0;
+        else if (obj[order[0]].len > cap) { set_err("oracle: output capacity too small"); rc = -1; }
+        else {
+            memcpy(out, obj[order[0]].buf, sizeof(int32_t) * (size_t)obj[order[0]].len);
+            *out_len = obj[order[0]].len;
+        }
+    }
+    beams_free(obj, order, bs);
+    return rc;
+}
+
+/* Every beam after the search, in beams order: lens[i], scores[i] and the
+ * tokens of beam i at out + i * cap. Test hook for the in-place reuse. */
+int or_beam_run(const or_model *m, const float *enc, int enc_len, const or_decode_params *p, int32_t *out, int cap,
+                int32_t *lens, float *scores, int32_t *nbeams_out, float *step_margin, int margin_cap) {
+    gobeam *obj; int *order, nbeams, tcap;
+    const int bs = p->beam_size <= 0 ? 1 : p->beam_size;
+    g_margin_out = step_margin;
+    g_margin_cap = step_margin ? margin_cap : 0;
+    int rc = beam_loop(m, enc, enc_len, p, &obj, &order, &nbeams, &tcap);
+    g_margin_out = NULL;
+    g_margin_cap = 0;
+    if (rc == 0) {
+        for (int i = 0; i < nbeams && rc == 0; i++) {
+            const gobeam *h = &obj[order[i]];
+            if (h->len > cap) { set_err("oracle: output capacity too small"); rc = -1; break; }
+            memcpy(out + (size_t)i * cap, h->buf, sizeof(int32_t) * (size_t)h->len);
+            lens[i] = h->len;
+            scores[i] = h->score;
+        }
+        *nbeams_out = nbeams;
+    }
+    beams_free(obj, order, bs);
     return rc;
 }
 

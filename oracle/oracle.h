@@ -23,10 +23,15 @@
  *                            brute-force sort.
  *   decoder loop           : decoder_test.go fixture behaviour + invariants
  *                            (P1/P2 self-attn collapse, P3 cross addressing).
+ *   beam prune             : Go's sort.Slice restated (pdqsort_func): sortedness
+ *                            and permutation by brute force, insertion-sort
+ *                            stability up to 12 items, hand-traced tie orders;
+ *                            in-place beam reuse: hand-derived histories.
  *   Parity unpinned        : end-to-end logits/tokens of the reference on any
  *                            configuration (no golden logits exist and the Go
  *                            toolchain is absent), sgemm summation order
- *                            (gonum / OpenBLAS), sort.Slice tie order.
+ *                            (gonum / OpenBLAS), and sort.Slice tie orders
+ *                            beyond the hand-traced cases.
  */
 #ifndef WHISPER_ORACLE_H
 #define WHISPER_ORACLE_H
@@ -102,6 +107,9 @@ void or_model_destroy(or_model *m);
 void or_model_hparams(const or_model *m, int32_t *out5);            /* vocab,state,head,layer,ctx */
 void or_model_set_eot(or_model *m, int32_t eot);                    /* model/decoder.go:85-94 */
 void or_model_set_fast_exp(or_model *m, int on);                    /* ml/attention.go:18-22 */
+/* n > 1: the forward's batch-1 GEMVs split their rows over n threads; every
+ * output element is the same dot as in the serial loop (fixture generation). */
+void or_model_set_forward_threads(or_model *m, int n);
 
 or_state *or_state_create(const or_model *m, const int32_t *prompt, int plen); /* decoder.go:306-365 */
 void or_state_destroy(or_state *s);
@@ -129,6 +137,18 @@ typedef struct {
  * length into out_len. Returns 0 on success. */
 int or_decode(const or_model *m, const float *enc, int enc_len, const or_decode_params *p,
               int32_t *out, int cap, int32_t *out_len);
+
+/* Beam search with every beam exposed (test hook for the in-place reuse of
+ * decoder.go:627-660): beam i's tokens at out + i*cap, lens[i], scores[i], in
+ * the order of the final beams slice; *nbeams = its length. step_margin (may be
+ * NULL) receives per step the smallest gap between different normalised scores
+ * among the first beam_size + 1 sorted candidates (INFINITY if none). */
+int or_beam_run(const or_model *m, const float *enc, int enc_len, const or_decode_params *p, int32_t *out, int cap,
+                int32_t *lens, float *scores, int32_t *nbeams, float *step_margin, int margin_cap);
+
+/* Go 1.25 sort.Slice (pdqsort_func) of n keys with less(i,j) = norm[i] > norm[j],
+ * carrying id[] along (the restatement the beam prune uses, decoder.go:1462-1475). */
+void or_go_sort_norm(float *norm, int32_t *id, int n);
 
 const char *or_last_error(void);
 

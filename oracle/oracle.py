@@ -61,6 +61,7 @@ def lib():
             "or_model_hparams": (None, [P, P]),
             "or_model_set_eot": (None, [P, C.c_int32]),
             "or_model_set_fast_exp": (None, [P, C.c_int]),
+            "or_model_set_forward_threads": (None, [P, C.c_int]),
             "or_state_create": (P, [P, P, C.c_int]),
             "or_state_destroy": (None, [P]),
             "or_state_reset": (None, [P, P, P, C.c_int]),
@@ -68,6 +69,8 @@ def lib():
             "or_forward": (C.c_int, [P, P, P, C.c_int, P]),
             "or_state_prepare_cross": (C.c_int, [P, P, P, C.c_int]),
             "or_decode": (C.c_int, [P, P, C.c_int, C.POINTER(OrDecodeParams), P, C.c_int, P]),
+            "or_beam_run": (C.c_int, [P, P, C.c_int, C.POINTER(OrDecodeParams), P, C.c_int, P, P, P, P, C.c_int]),
+            "or_go_sort_norm": (None, [P, P, C.c_int]),
             "or_last_error": (C.c_char_p, []),
         }
         for name, (res, args) in sig.items():
@@ -185,6 +188,22 @@ def topk(logits, k, temperature=1.0):
     return tok[:n], lp[:n]
 
 
+def go_sort_norm(norm, ids=None):
+    """Go's sort.Slice by norm descending (pdqsort); returns (norm, ids) in the sorted order."""
+    n = np.array(norm, np.float32, copy=True)
+    i = np.arange(n.size, dtype=np.int32) if ids is None else np.array(ids, np.int32, copy=True)
+    lib().or_go_sort_norm(_p(n), _p(i), n.size)
+    return n, i
+
+
+def _params(params):
+    prompt = (C.c_int32 * max(1, len(params.prompt)))(*params.prompt)
+    p = OrDecodeParams(C.cast(prompt, C.POINTER(C.c_int32)), len(params.prompt), params.beam_size,
+                       params.temperature, params.logprob_thold, params.no_speech_thold,
+                       int(params.no_fallback), params.max_tokens, int(params.suppress_nst))
+    return p, prompt
+
+
 class OracleModel:
     """or_model over a tensor table (objects with .name .type .shape .data)."""
 
@@ -221,21 +240,41 @@ class OracleModel:
     def set_fast_exp(self, on):
         lib().or_model_set_fast_exp(self._h, int(on))
 
+    def set_forward_threads(self, n):
+        lib().or_model_set_forward_threads(self._h, int(n))
+
     def state(self, tokens):
         return OracleState(self, tokens)
 
     def decode(self, enc, params):
         enc = np.ascontiguousarray(enc, np.float32)
-        prompt = (C.c_int32 * max(1, len(params.prompt)))(*params.prompt)
-        p = OrDecodeParams(C.cast(prompt, C.POINTER(C.c_int32)), len(params.prompt), params.beam_size,
-                           params.temperature, params.logprob_thold, params.no_speech_thold,
-                           int(params.no_fallback), params.max_tokens, int(params.suppress_nst))
-        cap = len(params.prompt) + self.n_ctx + 8
+        p, _keep = _params(params)
+        cap = len(params.prompt) + max(1, params.beam_size) * (self.n_ctx + 1) + 8
         out = np.empty(cap, np.int32)
         n = C.c_int32()
         if lib().or_decode(self._h, _p(enc), enc.shape[0], C.byref(p), _p(out), cap, C.byref(n)) != 0:
             raise RuntimeError(lib().or_last_error().decode())
         return [int(t) for t in out[:n.value]]
+
+    def beam_run(self, enc, params, margins=False):
+        """Every beam after the search: [(tokens, score)] in the final beams order
+        (and, with margins=True, the per-step selection margins)."""
+        enc = np.ascontiguousarray(enc, np.float32)
+        p, _keep = _params(params)
+        bs = max(1, params.beam_size)
+        cap = len(params.prompt) + bs * (self.n_ctx + 1) + 8
+        out = np.zeros((bs, cap), np.int32)
+        lens = np.zeros(bs, np.int32)
+        scores = np.zeros(bs, np.float32)
+        marg = np.full(self.n_ctx + 1, np.nan, np.float32)
+        nb = C.c_int32()
+        if lib().or_beam_run(self._h, _p(enc), enc.shape[0], C.byref(p), _p(out), cap, _p(lens), _p(scores),
+                             C.byref(nb), _p(marg), marg.size) != 0:
+            raise RuntimeError(lib().or_last_error().decode())
+        beams = [([int(t) for t in out[i, :lens[i]]], float(scores[i])) for i in range(nb.value)]
+        if margins:
+            return beams, [float(m) for m in marg if not np.isnan(m)]
+        return beams
 
 
 class OracleState:

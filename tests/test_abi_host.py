@@ -138,3 +138,24 @@ def test_gguf_roundtrip(wh, tmp_path):
 def test_decoder_params_defaults(wh):
     p = wh.DecoderParams()
     assert p.prompt == [] and p.beam_size == 0 and p.temperature == 0.0 and not p.no_fallback
+
+
+def test_gguf_parse_errors(wh, tmp_path):
+    """internal/gguf/gguf.go:69-135: bad magic, unsupported version and a
+    truncated header fail before any device work."""
+    lib = wh.native.lib()
+    h = C.c_void_p()
+    cases = {
+        "magic": b"GGUX" + b"\0" * 28,
+        "version": b"GGUF" + (7).to_bytes(4, "little") + b"\0" * 24,
+        "truncated": b"GGUF" + (3).to_bytes(4, "little") + (1).to_bytes(8, "little") + (5).to_bytes(8, "little")
+        + b"\x05\0\0\0\0\0\0\0abc",
+    }
+    want = {"magic": (wh.native.WH_ERR_INVALID, b"invalid magic"),
+            "version": (wh.native.WH_ERR_UNSUPPORTED, b"unsupported version"),
+            "truncated": (wh.native.WH_ERR_INVALID, b"truncated")}
+    for name, blob in cases.items():
+        path = tmp_path / f"{name}.gguf"
+        path.write_bytes(blob)
+        rc = lib.wh_model_load_gguf(str(path).encode(), 0, C.byref(h))
+        assert (rc, want[name][1] in lib.wh_last_error()) == (want[name][0], True), name

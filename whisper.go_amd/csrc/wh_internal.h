@@ -145,21 +145,25 @@ struct SampleBufs {
     float *part_val2;    // [S][P] best excluding eot
     int32_t *part_idx2;
     int parts;
+    // per-stream sampling parameters (DecoderParams of each stream)
+    float *inv_temp;     // [S] 1 / temperature
+    int32_t *supp;       // [S] SuppressNST
+    float *nst;          // [S] NoSpeechThold
 };
 int launch_penalty_argmax(const float *logits, const int32_t *hist, const int32_t *hist_len, int hist_cap,
-                          const int32_t *active, int S, int V, float inv_temp, int eot, const SampleBufs &b,
-                          hipStream_t st);
-int launch_argmax_final(const SampleBufs &b, const float *cur, int S, int V, int eot, int suppress_nst,
-                        float no_speech_thold, const int32_t *active, int32_t *hist, int32_t *hist_len,
-                        int hist_cap, int32_t *tok, int32_t *pos, int32_t *out_ids, hipStream_t st);
+                          const int32_t *active, int S, int V, int eot, const SampleBufs &b, hipStream_t st);
+int launch_argmax_final(const SampleBufs &b, const float *cur, int S, int V, int eot, const int32_t *active,
+                        int32_t *hist, int32_t *hist_len, int hist_cap, int32_t *tok, int32_t *pos, int32_t *out_ids,
+                        hipStream_t st);
 // Exact top-k of rows whose k_topk result has ties (the reference's replace-min scan).
 int launch_topk_ties(const float *cur, const int32_t *active, int S, int V, int k, int kk, float inv_temp,
                      const float *logz, int32_t *tok, float *lp, hipStream_t st);
-// One beam step's candidate ranking, prune and history rewrite on the device.
-int launch_beam_select(const int32_t *ttok, const float *tlp, int k, int kk, const int32_t *hist_in,
-                       const int32_t *len_in, int32_t *hist_out, int32_t *len_out, int cap, float *score,
-                       int32_t *nbeams, int32_t *active, int32_t *tok, int32_t *pos, int32_t *stop,
-                       const float *powtab, int bs, int eot, hipStream_t st);
+// One beam step's candidate ranking (Go's sort.Slice order), prune and in-place
+// reuse of the beam objects' histories on the device.
+int launch_beam_select(const int32_t *ttok, const float *tlp, int k, int kk, int32_t *hist, int32_t *len,
+                       int32_t *gcap, int cap, float *score, int32_t *order, int32_t *nbeams, int32_t *active,
+                       int32_t *tok, int32_t *pos, int32_t *stop, const float *powtab, int bs, int eot, int n_ctx,
+                       hipStream_t st);
 // top-k scratch: TOPK_ROWS_MAX x TOPK_PARTS partitions x (2 + 2 * 8) floats
 constexpr int TOPK_ROWS_MAX = 16, TOPK_PARTS = 32, TOPK_SCRATCH_FLOATS = TOPK_ROWS_MAX * TOPK_PARTS * 18;
 int launch_topk(const float *cur, const int32_t *active, int S, int V, int k, float inv_temp, int32_t *out_tok,

@@ -1472,13 +1472,14 @@ __device__ __forceinline__ void better(float v, int i, float &bv, int &bi) {
 
 __global__ __launch_bounds__(256) void k_penalty_argmax(const float *logits, const int32_t *hist,
                                                         const int32_t *hist_len, int hist_cap, const int32_t *active,
-                                                        int V, float inv_temp, int eot, float *cur, float *pval,
+                                                        int V, const float *inv_temps, int eot, float *cur, float *pval,
                                                         int32_t *pidx, float *pval2, int32_t *pidx2, int parts) {
     __shared__ int32_t win[PEN_WINDOW];
     __shared__ float rv[4], rv2[4];
     __shared__ int ri[4], ri2[4];
     const int s = blockIdx.y, part = blockIdx.x;
     if (active && !active[s]) return;
+    const float inv_temp = inv_temps[s];
     const int len = hist_len[s];
     const int start = len > PEN_WINDOW ? len - PEN_WINDOW : 0;
     const int nwin = len - start;
@@ -1522,9 +1523,9 @@ __global__ __launch_bounds__(256) void k_penalty_argmax(const float *logits, con
 }
 
 __global__ void k_argmax_final(const float *pval, const int32_t *pidx, const float *pval2, const int32_t *pidx2,
-                               int parts, const float *cur, int V, int eot, int suppress_nst, float nst,
-                               const int32_t *active, int32_t *hist, int32_t *hist_len, int hist_cap, int32_t *tok,
-                               int32_t *pos, int32_t *out_ids) {
+                               int parts, const float *cur, int V, int eot, const int32_t *suppress_nsts,
+                               const float *nsts, const int32_t *active, int32_t *hist, int32_t *hist_len,
+                               int hist_cap, int32_t *tok, int32_t *pos, int32_t *out_ids) {
     const int s = blockIdx.x;
     if (threadIdx.x != 0) return;
     if (active && !active[s]) { if (out_ids) out_ids[s] = -1; return; }
@@ -1536,8 +1537,10 @@ __global__ void k_argmax_final(const float *pval, const int32_t *pidx, const flo
     }
     if (bi == 0x7FFFFFFF) bi = 0;  // all values NaN: the reference keeps index 0
     int id = bi;
-    if (suppress_nst && eot >= 0 && eot < V) {
-        if (cur[(size_t)s * V + eot] < -nst && id == eot) id = (bi2 == 0x7FFFFFFF) ? eot : bi2;
+    // SuppressNST (decoder.go:1016-1034): an EOT below -NoSpeechThold is replaced by
+    // the best other token
+    if (suppress_nsts[s] && eot >= 0 && eot < V) {
+        if (cur[(size_t)s * V + eot] < -nsts[s] && id == eot) id = (bi2 == 0x7FFFFFFF) ? eot : bi2;
     }
     int len = hist_len[s];
     if (len < hist_cap) hist[(size_t)s * hist_cap + len] = id;
@@ -1548,20 +1551,18 @@ __global__ void k_argmax_final(const float *pval, const int32_t *pidx, const flo
 }
 
 int launch_penalty_argmax(const float *logits, const int32_t *hist, const int32_t *hist_len, int hist_cap,
-                          const int32_t *active, int S, int V, float inv_temp, int eot, const SampleBufs &b,
-                          hipStream_t st) {
+                          const int32_t *active, int S, int V, int eot, const SampleBufs &b, hipStream_t st) {
     hipLaunchKernelGGL(k_penalty_argmax, dim3(b.parts, S), dim3(256), 0, st, logits, hist, hist_len, hist_cap,
-                       active, V, inv_temp, eot, b.cur, b.part_val, b.part_idx, b.part_val2, b.part_idx2, b.parts);
+                       active, V, b.inv_temp, eot, b.cur, b.part_val, b.part_idx, b.part_val2, b.part_idx2, b.parts);
     WH_HIP(hipGetLastError());
     return WH_OK;
 }
 
-int launch_argmax_final(const SampleBufs &b, const float *cur, int S, int V, int eot, int suppress_nst,
-                        float no_speech_thold, const int32_t *active, int32_t *hist, int32_t *hist_len, int hist_cap,
-                        int32_t *tok, int32_t *pos, int32_t *out_ids, hipStream_t st) {
+int launch_argmax_final(const SampleBufs &b, const float *cur, int S, int V, int eot, const int32_t *active,
+                        int32_t *hist, int32_t *hist_len, int hist_cap, int32_t *tok, int32_t *pos, int32_t *out_ids,
+                        hipStream_t st) {
     hipLaunchKernelGGL(k_argmax_final, dim3(S), dim3(64), 0, st, b.part_val, b.part_idx, b.part_val2, b.part_idx2,
-                       b.parts, cur, V, eot, suppress_nst, no_speech_thold, active, hist, hist_len, hist_cap, tok, pos,
-                       out_ids);
+                       b.parts, cur, V, eot, b.supp, b.nst, active, hist, hist_len, hist_cap, tok, pos, out_ids);
     WH_HIP(hipGetLastError());
     return WH_OK;
 }
@@ -1771,98 +1772,297 @@ __global__ __launch_bounds__(64) void k_topk_ties(const float *cur, const int32_
     }
 }
 
-// One beam step's prune (decoder.go:578-660): every live hypothesis b < *nbeams
-// proposes its k candidates (score + logprob, normalised by len^0.6 with len the
-// new length), a finished one (last token EOT) proposes itself; candidates are
-// ranked by normalised score, descending, ties in proposal order (a stable sort;
-// Go's sort.Slice is not stable, the order among exact ties is a documented
-// choice), the first bs become the next hypotheses. Their histories go to the
-// other history buffer; the current token, position, activity, score and count
-// are updated in place, and *stop is set when every hypothesis has finished or
-// the first one repeats its last token more than 20 times (decoder.go:703-718).
+// ---- Go's sort.Slice on the device (one lane) ---------------------------------------
+// The beam prune sorts its candidates with Go's sort.Slice (decoder.go:1462-1475),
+// which is pdqsort (Go 1.25 src/sort/zsortfunc.go) and not stable: the order it
+// leaves equal normalised scores in decides which parent lands in which slot.
+// This is that algorithm step by step over an index permutation ix of LDS keys,
+// less(i, j) = key[ix[i]] > key[ix[j]]. Sorting disjoint ranges in another order
+// gives the same result (a range only ever compares with its fixed left
+// neighbour), so the recursion runs from an explicit stack.
+struct GoSort {
+    const float *key;
+    int *ix;
+    __device__ bool less(int i, int j) const { return key[ix[i]] > key[ix[j]]; }
+    __device__ void swap(int i, int j) const { const int t = ix[i]; ix[i] = ix[j]; ix[j] = t; }
+    __device__ void insertion(int a, int b) const {
+        for (int i = a + 1; i < b; i++)
+            for (int j = i; j > a && less(j, j - 1); j--) swap(j, j - 1);
+    }
+    __device__ void sift_down(int lo, int hi, int first) const {
+        int root = lo;
+        for (;;) {
+            int child = 2 * root + 1;
+            if (child >= hi) return;
+            if (child + 1 < hi && less(first + child, first + child + 1)) child++;
+            if (!less(first + root, first + child)) return;
+            swap(first + root, first + child);
+            root = child;
+        }
+    }
+    __device__ void heapsort(int a, int b) const {
+        const int hi = b - a;
+        for (int i = (hi - 1) / 2; i >= 0; i--) sift_down(i, hi, a);
+        for (int i = hi - 1; i >= 0; i--) { swap(a, a + i); sift_down(0, i, a); }
+    }
+    // median of three by three order-2 steps, counting swaps
+    __device__ int median(int a, int b, int c, int &swaps) const {
+        if (less(b, a)) { swaps++; const int t = a; a = b; b = t; }
+        if (less(c, b)) { swaps++; const int t = b; b = c; c = t; }
+        if (less(b, a)) { swaps++; const int t = a; a = b; b = t; }
+        return b;
+    }
+    // hint: 0 unknown, 1 increasing, 2 decreasing
+    __device__ int choose_pivot(int a, int b, int &hint) const {
+        const int l = b - a;
+        int swaps = 0, i = a + l / 4, j = a + l / 4 * 2, k = a + l / 4 * 3;
+        if (l >= 8) {
+            if (l >= 50) {
+                i = median(i - 1, i, i + 1, swaps);
+                j = median(j - 1, j, j + 1, swaps);
+                k = median(k - 1, k, k + 1, swaps);
+            }
+            j = median(i, j, k, swaps);
+        }
+        hint = swaps == 0 ? 1 : (swaps == 12 ? 2 : 0);
+        return j;
+    }
+    __device__ bool partial_insertion(int a, int b) const {
+        int i = a + 1;
+        for (int step = 0; step < 5; step++) {
+            while (i < b && !less(i, i - 1)) i++;
+            if (i == b) return true;
+            if (b - a < 50) return false;
+            swap(i, i - 1);
+            if (i - a >= 2)
+                for (int j = i - 1; j >= 1; j--) {
+                    if (!less(j, j - 1)) break;
+                    swap(j, j - 1);
+                }
+            if (b - i >= 2)
+                for (int j = i + 1; j < b; j++) {
+                    if (!less(j, j - 1)) break;
+                    swap(j, j - 1);
+                }
+        }
+        return false;
+    }
+    __device__ void break_patterns(int a, int b) const {
+        const int length = b - a;
+        if (length < 8) return;
+        uint64_t r = (uint64_t)length;
+        const unsigned modulus = 1u << (32 - __clz(length));
+        const int idx = a + (length / 4) * 2 - 1;
+        for (int i = 0; i < 3; i++) {
+            r ^= r << 13;
+            r ^= r >> 7;
+            r ^= r << 17;
+            int other = (int)((unsigned)r & (modulus - 1));
+            if (other >= length) other -= length;
+            swap(idx - 1 + i, a + other);
+        }
+    }
+    __device__ int partition_equal(int a, int b, int pivot) const {
+        swap(a, pivot);
+        int i = a + 1, j = b - 1;
+        for (;;) {
+            while (i <= j && !less(a, i)) i++;
+            while (i <= j && less(a, j)) j--;
+            if (i > j) break;
+            swap(i, j);
+            i++;
+            j--;
+        }
+        return i;
+    }
+    __device__ int partition(int a, int b, int pivot, bool &already) const {
+        swap(a, pivot);
+        int i = a + 1, j = b - 1;
+        while (i <= j && less(i, a)) i++;
+        while (i <= j && !less(j, a)) j--;
+        if (i > j) {
+            swap(j, a);
+            already = true;
+            return j;
+        }
+        swap(i, j);
+        i++;
+        j--;
+        for (;;) {
+            while (i <= j && less(i, a)) i++;
+            while (i <= j && !less(j, a)) j--;
+            if (i > j) break;
+            swap(i, j);
+            i++;
+            j--;
+        }
+        swap(j, a);
+        already = false;
+        return j;
+    }
+    // Returns false if the frame stack would overflow (cannot happen below 2^16 items).
+    __device__ bool sort(int n) const {
+        constexpr int STACK = 48;
+        int sa[STACK], sb[STACK], sl[STACK];
+        int sp = 0;
+        sa[sp] = 0; sb[sp] = n; sl[sp] = n > 0 ? 32 - __clz(n) : 0; sp++;
+        while (sp > 0) {
+            sp--;
+            int a = sa[sp], b = sb[sp], limit = sl[sp];
+            bool balanced = true, partitioned = true;
+            for (;;) {
+                const int length = b - a;
+                if (length <= 12) { insertion(a, b); break; }
+                if (limit == 0) { heapsort(a, b); break; }
+                if (!balanced) { break_patterns(a, b); limit--; }
+                int hint;
+                int pivot = choose_pivot(a, b, hint);
+                if (hint == 2) {
+                    for (int i = a, j = b - 1; i < j; i++, j--) swap(i, j);
+                    pivot = (b - 1) - (pivot - a);
+                    hint = 1;
+                }
+                if (balanced && partitioned && hint == 1 && partial_insertion(a, b)) break;
+                if (a > 0 && !less(a - 1, pivot)) { a = partition_equal(a, b, pivot); continue; }
+                bool already;
+                const int mid = partition(a, b, pivot, already);
+                partitioned = already;
+                const int left = mid - a, right = b - mid, thr = length / 8;
+                if (sp == STACK) return false;
+                if (left < right) {
+                    balanced = left >= thr;
+                    sa[sp] = a; sb[sp] = mid; sl[sp] = limit; sp++;
+                    a = mid + 1;
+                } else {
+                    balanced = right >= thr;
+                    sa[sp] = mid + 1; sb[sp] = b; sl[sp] = limit; sp++;
+                    b = mid;
+                }
+            }
+        }
+        return true;
+    }
+};
+
+// One beam step's prune and next hypotheses (decoder.go:575-718). The hypotheses
+// are beam objects: object o has its own token history hist[o][0..len[o]) with
+// Go's slice capacity gcap[o], and a score; order[0..*nbeams) is the beams slice.
+// Each live object in that order proposes its k candidates (its top-k rows of
+// ttok/tlp, normalised by (len+1)^0.6), a finished one (last token EOT) proposes
+// itself. Candidates are sorted with Go's sort.Slice (above); the first bs are
+// applied in slot order exactly as the reference's loop does: slot i reuses the
+// object of beams[nbeams-1-i] (popped from the end of reusableBeams), reads its
+// parent as earlier slots left it, and an object too small for the new length
+// gets a fresh zeroed slice (make) first, which a self-parent then copies onto
+// itself. Then tok, pos and active of every object are set for the next forward,
+// and stop[0] = 1 when every hypothesis has finished or the first repeats its
+// last token more than 20 times (decoder.go:690-718). stop[1] is the position
+// of the first live hypothesis at or past n_ctx (the reference's forward fails
+// there on the next step), else -1; such a hypothesis is not made active.
 // powtab[n] = float(pow(n, 0.6)) as the host computes it. A stopped state is left
 // as it is.
 __global__ __launch_bounds__(256) void k_beam_select(const int32_t *ttok, const float *tlp, int k, int kk,
-                                                     const int32_t *hist_in, const int32_t *len_in,
-                                                     int32_t *hist_out, int32_t *len_out, int cap, float *score,
-                                                     int32_t *nbeams, int32_t *active, int32_t *tok, int32_t *pos,
-                                                     int32_t *stop, const float *powtab, int bs, int eot) {
-    __shared__ float cnorm[BEAM_MAX * TOPK_MAX], cscore[BEAM_MAX * TOPK_MAX], clp[BEAM_MAX * TOPK_MAX];
-    __shared__ int cpar[BEAM_MAX * TOPK_MAX], ctok[BEAM_MAX * TOPK_MAX];
-    __shared__ int sel[BEAM_MAX];
-    __shared__ int ncand, nkeep;
+                                                     int32_t *hist, int32_t *len, int32_t *gcap, int cap,
+                                                     float *score, int32_t *order, int32_t *nbeams, int32_t *active,
+                                                     int32_t *tok, int32_t *pos, int32_t *stop, const float *powtab,
+                                                     int bs, int eot, int n_ctx) {
+    constexpr int NCAND = BEAM_MAX * (TOPK_MAX - 1);
+    __shared__ float cnorm[NCAND], cscore[NCAND], clp[NCAND];
+    __shared__ int cpar[NCAND], ctok[NCAND], cix[NCAND];
+    __shared__ int reuse[BEAM_MAX], next[BEAM_MAX];
+    __shared__ int nkeep, nbin, s_nb, s_par, s_cpy, s_zero, s_bad;
     const int t = threadIdx.x;
-    if (*stop) return;
+    if (stop[0]) return;
     if (t == 0) {
         const int nb = *nbeams;
         int n = 0;
         for (int b = 0; b < nb; b++) {
-            const int L = len_in[b];
-            const int last = L > 0 ? hist_in[(size_t)b * cap + L - 1] : -1;
-            const float sc = score[b];
+            const int o = order[b];
+            reuse[b] = o;
+            const int L = len[o];
+            const int last = L > 0 ? hist[(size_t)o * cap + L - 1] : -1;
+            const float sc = score[o];
             if (last == eot) {
-                cpar[n] = b; cscore[n] = sc; ctok[n] = eot; clp[n] = 0.0f; cnorm[n] = sc / powtab[L];
+                cpar[n] = o; cscore[n] = sc; ctok[n] = eot; clp[n] = 0.0f; cnorm[n] = sc / powtab[L];
                 n++;
             } else {
                 for (int c = 0; c < k; c++) {
-                    const float lpc = tlp[(size_t)b * kk + c];
+                    const float lpc = tlp[(size_t)o * kk + c];
                     const float ns = sc + lpc;
-                    cpar[n] = b; cscore[n] = ns; ctok[n] = ttok[(size_t)b * kk + c]; clp[n] = lpc;
+                    cpar[n] = o; cscore[n] = ns; ctok[n] = ttok[(size_t)o * kk + c]; clp[n] = lpc;
                     cnorm[n] = ns / powtab[L + 1];
                     n++;
                 }
             }
         }
-        ncand = n;
-        nkeep = min(n, bs);
-    }
-    if (t < BEAM_MAX) sel[t] = 0;  // every kept slot is written below; a NaN score cannot leave one unset
-    __syncthreads();
-    const int n = ncand, keep = nkeep;
-    if (t < n) {
-        const float v = cnorm[t];
-        int r = 0;
-        for (int j = 0; j < n; j++) r += (cnorm[j] > v) || (cnorm[j] == v && j < t);
-        if (r < keep) sel[r] = t;
+        for (int i = 0; i < n; i++) cix[i] = i;
+        const GoSort gs{cnorm, cix};
+        s_bad = gs.sort(n) ? 0 : 1;
+        nbin = nb;
+        nkeep = min(min(n, bs), nb);
     }
     __syncthreads();
-    for (int r = 0; r < keep; r++) {
-        const int c = sel[r], par = cpar[c];
-        const int L = len_in[par];
-        for (int j = t; j < L; j += blockDim.x) hist_out[(size_t)r * cap + j] = hist_in[(size_t)par * cap + j];
-    }
-    if (t == 0) {
-        for (int r = 0; r < keep; r++) {
-            const int c = sel[r], par = cpar[c];
-            const int L = len_in[par];
-            const int last = L > 0 ? hist_in[(size_t)par * cap + L - 1] : -1;
-            // a finished hypothesis carried over keeps its tokens (decoder.go:644-651)
+    const int keep = nkeep;
+    for (int i = 0; i < keep; i++) {
+        if (t == 0) {
+            const int c = cix[i];
+            const int o = reuse[nbin - 1 - i];  // reusableBeams[n-1], popped
+            const int par = cpar[c];
+            const int L = len[par];
+            const int last = L > 0 ? hist[(size_t)par * cap + L - 1] : -1;
             const bool carry = last == eot && ctok[c] == eot && clp[c] == 0.0f;
-            const int Ln = carry ? L : L + 1;
-            if (!carry) hist_out[(size_t)r * cap + L] = ctok[c];
-            const int lt = carry ? last : ctok[c];
-            len_out[r] = Ln;
-            score[r] = cscore[c];
-            tok[r] = lt;
-            pos[r] = Ln - 1;
-            active[r] = lt != eot;
+            const int need = carry ? L : L + 1;
+            // make([]int32, need) when the capacity is short; a self-parent then copies the zeros
+            s_zero = (gcap[o] < need && o == par) ? need : 0;
+            if (gcap[o] < need) gcap[o] = need;
+            s_cpy = (o != par) ? (carry ? need : need - 1) : 0;
+            s_nb = o;
+            s_par = par;
+            next[i] = o;
+            len[o] = need;
+            score[o] = cscore[c];
+            // the appended token (written after the copy below)
+            cix[i] = carry ? -1 : ctok[c];
         }
-        for (int r = keep; r < bs; r++) active[r] = 0;
-        *nbeams = keep;
+        __syncthreads();
+        const int o = s_nb, par = s_par, nz = s_zero, nc = s_cpy;
+        for (int j = t; j < nz; j += blockDim.x) hist[(size_t)o * cap + j] = 0;
+        for (int j = t; j < nc; j += blockDim.x) hist[(size_t)o * cap + j] = hist[(size_t)par * cap + j];
+        __syncthreads();
+        if (t == 0 && cix[i] >= 0) hist[(size_t)o * cap + len[o] - 1] = cix[i];
+        __syncthreads();
     }
-    __syncthreads();
     if (t == 0) {
-        bool all = true;
-        for (int r = 0; r < keep; r++) all &= (tok[r] == eot);
-        bool halt = all || keep == 0;
-        const int L0 = keep > 0 ? len_out[0] : 0;
-        if (!halt && L0 >= 2) {
-            const int32_t *h0 = hist_out;
-            int streak = 1;
-            for (int i = L0 - 2; i >= 0 && h0[i] == h0[L0 - 1]; i--)
-                if (++streak > 20) { halt = true; break; }
+        int bad_pos = -1;
+        for (int i = 0; i < keep; i++) {
+            const int o = next[i];
+            order[i] = o;
+            const int L = len[o];
+            const int lt = L > 0 ? hist[(size_t)o * cap + L - 1] : -1;
+            tok[o] = lt;
+            pos[o] = L - 1;
+            const bool live = lt != eot;
+            if (live && L - 1 >= n_ctx && bad_pos < 0) bad_pos = L - 1;
+            active[o] = live && L - 1 < n_ctx;
         }
-        *stop = halt ? 1 : 0;
+        // objects left out of the beams slice (never with at least one candidate per hypothesis)
+        for (int i = keep; i < nbin; i++) active[reuse[nbin - 1 - i]] = 0;
+        *nbeams = keep;
+        bool all = true;
+        for (int i = 0; i < keep; i++) all &= (tok[next[i]] == eot);
+        bool halt = all || keep == 0;
+        if (!halt && keep > 0) {
+            const int o = next[0], L0 = len[o];
+            const int32_t *h0 = hist + (size_t)o * cap;
+            if (L0 >= 2) {
+                int streak = 1;
+                for (int i = L0 - 2; i >= 0 && h0[i] == h0[L0 - 1]; i--)
+                    if (++streak > 20) { halt = true; break; }
+            }
+        }
+        stop[0] = halt ? 1 : (s_bad ? 1 : 0);
+        stop[1] = bad_pos;
+        stop[2] = s_bad;
     }
 }
 
@@ -1874,14 +2074,14 @@ int launch_topk_ties(const float *cur, const int32_t *active, int S, int V, int 
     return WH_OK;
 }
 
-int launch_beam_select(const int32_t *ttok, const float *tlp, int k, int kk, const int32_t *hist_in,
-                       const int32_t *len_in, int32_t *hist_out, int32_t *len_out, int cap, float *score,
-                       int32_t *nbeams, int32_t *active, int32_t *tok, int32_t *pos, int32_t *stop,
-                       const float *powtab, int bs, int eot, hipStream_t st) {
-    if (bs < 1 || bs > BEAM_MAX || k < 1 || k >= kk || kk > TOPK_MAX || BEAM_MAX * k > 256)
+int launch_beam_select(const int32_t *ttok, const float *tlp, int k, int kk, int32_t *hist, int32_t *len,
+                       int32_t *gcap, int cap, float *score, int32_t *order, int32_t *nbeams, int32_t *active,
+                       int32_t *tok, int32_t *pos, int32_t *stop, const float *powtab, int bs, int eot, int n_ctx,
+                       hipStream_t st) {
+    if (bs < 1 || bs > BEAM_MAX || k < 1 || k >= kk || kk > TOPK_MAX)
         return fail(WH_ERR_INVALID, "beam: unsupported beam size");
-    hipLaunchKernelGGL(k_beam_select, dim3(1), dim3(256), 0, st, ttok, tlp, k, kk, hist_in, len_in, hist_out, len_out,
-                       cap, score, nbeams, active, tok, pos, stop, powtab, bs, eot);
+    hipLaunchKernelGGL(k_beam_select, dim3(1), dim3(256), 0, st, ttok, tlp, k, kk, hist, len, gcap, cap, score, order,
+                       nbeams, active, tok, pos, stop, powtab, bs, eot, n_ctx);
     WH_HIP(hipGetLastError());
     return WH_OK;
 }

@@ -455,25 +455,24 @@ __device__ __forceinline__ void ll_load_scaled(float (&x)[K], float *xo, const u
     store_scaled<K>(x, w, n, xo);
 }
 
-// Mean and 1/sd of the n values x[k] = element lane + 64k in one pass: the
-// sums of x and x*x reduce side by side (half the dependent chain of the
-// two-pass form, so it stays under the dots it overlaps), var = E[x^2] - mean^2.
-// LayerNorm inputs have a spread comparable to or above their mean, so the
-// subtraction loses no significant bits.
+// Mean and 1/sd of the n values x[k] = element lane + 64k, in two passes as the
+// reference computes them (internal/ml/ops.go:166-193): the mean, then the mean
+// of squared deviations, sqrt in float64. A one-pass E[x^2] - mean^2 loses the
+// variance to cancellation once |mean| is ~100x the spread. The communication
+// wave computes them while the compute waves run the folded dots.
 template <int K>
 __device__ __forceinline__ void ln_stats(const float (&x)[K], int n, float &mean, float &rsd) {
     const int lane = tid() & 63;
-    float s[K], q[K];
+    float t[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) t[k] = (lane + 64 * k < n) ? x[k] : 0.0f;
+    mean = wave_sum(tree_sum<K>(t)) / (float)n;
 #pragma unroll
     for (int k = 0; k < K; k++) {
-        const float v = (lane + 64 * k < n) ? x[k] : 0.0f;
-        s[k] = v;
-        q[k] = v * v;
+        const float u = x[k] - mean;
+        t[k] = (lane + 64 * k < n) ? u * u : 0.0f;
     }
-    const float S = wave_sum(tree_sum<K>(s)), Q = wave_sum(tree_sum<K>(q));
-    const float inv_n = 1.0f / (float)n;
-    mean = S * inv_n;
-    const float var = fmaxf(Q * inv_n - mean * mean, 0.0f);
+    const float var = wave_sum(tree_sum<K>(t)) / (float)n;
     rsd = 1.0f / (float)sqrt((double)(var + 1e-5f));
 }
 

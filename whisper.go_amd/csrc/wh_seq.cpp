@@ -44,6 +44,8 @@ struct wh_seq {
     std::vector<int32_t> h_len;     // host mirror of hist_len
     std::vector<int32_t> h_active;  // host mirror of active
     std::vector<std::vector<int32_t>> h_hist;  // host mirror of the histories
+    std::vector<float> h_inv, h_nst;  // host mirrors of the per-stream sampling parameters
+    std::vector<int32_t> h_supp;
     int32_t *pinned_ids = nullptr;
 
     // persistent decode kernel (one stream, reference mask, uniform weight type)
@@ -449,6 +451,32 @@ int mega_run(wh_seq &s, int n, float inv_temp, int suppress_nst, float nst, int 
     return WH_OK;
 }
 
+// Per-stream sampling parameters for the sampling kernels; uploaded only when
+// they change. Arrays of S entries.
+int set_sample_params(wh_seq &s, const float *inv, const int32_t *supp, const float *nst) {
+    bool same = true;
+    for (int i = 0; i < s.S; i++)
+        same &= s.h_inv[i] == inv[i] && s.h_supp[i] == (supp[i] != 0) && s.h_nst[i] == nst[i];
+    if (same) return WH_OK;
+    for (int i = 0; i < s.S; i++) {
+        s.h_inv[i] = inv[i];
+        s.h_supp[i] = supp[i] != 0;
+        s.h_nst[i] = nst[i];
+    }
+    WH_HIP(hipMemcpyAsync(s.sb.inv_temp, s.h_inv.data(), sizeof(float) * s.S, hipMemcpyHostToDevice, s.st));
+    WH_HIP(hipMemcpyAsync(s.sb.supp, s.h_supp.data(), sizeof(int32_t) * s.S, hipMemcpyHostToDevice, s.st));
+    WH_HIP(hipMemcpyAsync(s.sb.nst, s.h_nst.data(), sizeof(float) * s.S, hipMemcpyHostToDevice, s.st));
+    // the host vectors are the copies' sources: they must not change before the copies ran
+    WH_HIP(hipStreamSynchronize(s.st));
+    return WH_OK;
+}
+
+int set_sample_params_all(wh_seq &s, float inv, int32_t supp, float nst) {
+    std::vector<float> a(s.S, inv), c(s.S, nst);
+    std::vector<int32_t> b(s.S, supp);
+    return set_sample_params(s, a.data(), b.data(), c.data());
+}
+
 int upload_active(wh_seq &s, const int32_t *active) {
     for (int i = 0; i < s.S; i++) s.h_active[i] = active ? (active[i] != 0) : 1;
     WH_HIP(hipMemcpyAsync(s.active, s.h_active.data(), sizeof(int32_t) * s.S, hipMemcpyHostToDevice, s.st));
@@ -517,6 +545,9 @@ int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t e
     ALLOC(s->sb.part_idx, (size_t)S * SAMPLE_PARTS);
     ALLOC(s->sb.part_val2, (size_t)S * SAMPLE_PARTS);
     ALLOC(s->sb.part_idx2, (size_t)S * SAMPLE_PARTS);
+    ALLOC(s->sb.inv_temp, (size_t)S);
+    ALLOC(s->sb.supp, (size_t)S);
+    ALLOC(s->sb.nst, (size_t)S);
     ALLOC(s->hist, (size_t)S * s->hist_cap);
     ALLOC(s->hist_len, (size_t)S);
     ALLOC(s->tok, (size_t)S);
@@ -536,6 +567,16 @@ int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t e
     s->h_len.assign(S, 0);
     s->h_active.assign(S, 1);
     s->h_hist.assign(S, {});
+    s->h_inv.assign(S, 1.0f);
+    s->h_supp.assign(S, 0);
+    s->h_nst.assign(S, 0.0f);
+    {
+        std::vector<int32_t> z(S, 0);
+        std::vector<float> one(S, 1.0f), zf(S, 0.0f);
+        WH_HIP(hipMemcpy(s->sb.inv_temp, one.data(), sizeof(float) * S, hipMemcpyHostToDevice));
+        WH_HIP(hipMemcpy(s->sb.supp, z.data(), sizeof(int32_t) * S, hipMemcpyHostToDevice));
+        WH_HIP(hipMemcpy(s->sb.nst, zf.data(), sizeof(float) * S, hipMemcpyHostToDevice));
+    }
     // cross K/V projections of every encoder output (decoder.go:923-940), once per sequence
     float *enc = nullptr;
     WH_HIP(hipMalloc(&enc, sizeof(float) * (size_t)enc_len * d));
@@ -613,16 +654,14 @@ static int seq_forward_active(wh_seq *s, const int32_t *active) {
     return seq_forward(*s);
 }
 
-int seq_step_greedy(wh_seq *s, const int32_t *active, float temperature, int32_t suppress_nst, float nst,
-                    int32_t *out_ids, float *out_logits) {
-    if (!s) return fail(WH_ERR_INVALID, "seq: null handle");
-    WH_HIP(hipSetDevice(s->m->device));
+// One greedy step of the active streams with the sampling parameters already
+// set per stream (set_sample_params).
+static int step_greedy_impl(wh_seq *s, const int32_t *active, int32_t *out_ids, float *out_logits) {
     int rc;
-    const float inv = temperature > 0 ? 1.0f / temperature : 1.0f;
     if (mega_eligible(s, active)) {
         int got = 0;
-        if ((rc = mega_run(*s, 1, inv, suppress_nst, nst, s->hist_cap, -1, 0, out_logits, out_ids, &got, nullptr,
-                           nullptr)))
+        if ((rc = mega_run(*s, 1, s->h_inv[0], s->h_supp[0], s->h_nst[0], s->hist_cap, -1, 0, out_logits, out_ids,
+                           &got, nullptr, nullptr)))
             return rc;
         return WH_OK;
     }
@@ -630,11 +669,11 @@ int seq_step_greedy(wh_seq *s, const int32_t *active, float temperature, int32_t
     const int V = s->m->n_vocab;
     {
         Prof p(*s, "sample", 0);
-        if ((rc = launch_penalty_argmax(s->logits, s->hist, s->hist_len, s->hist_cap, s->active, s->S, V, inv,
-                                        s->m->eot, s->sb, s->st)))
+        if ((rc = launch_penalty_argmax(s->logits, s->hist, s->hist_len, s->hist_cap, s->active, s->S, V, s->m->eot,
+                                        s->sb, s->st)))
             return rc;
-        if ((rc = launch_argmax_final(s->sb, s->sb.cur, s->S, V, s->m->eot, suppress_nst, nst, s->active, s->hist,
-                                      s->hist_len, s->hist_cap, s->tok, s->pos, s->out_ids, s->st)))
+        if ((rc = launch_argmax_final(s->sb, s->sb.cur, s->S, V, s->m->eot, s->active, s->hist, s->hist_len,
+                                      s->hist_cap, s->tok, s->pos, s->out_ids, s->st)))
             return rc;
     }
     WH_HIP(hipMemcpyAsync(s->pinned_ids, s->out_ids, sizeof(int32_t) * s->S, hipMemcpyDeviceToHost, s->st));
@@ -650,6 +689,16 @@ int seq_step_greedy(wh_seq *s, const int32_t *active, float temperature, int32_t
         }
     }
     return WH_OK;
+}
+
+int seq_step_greedy(wh_seq *s, const int32_t *active, float temperature, int32_t suppress_nst, float nst,
+                    int32_t *out_ids, float *out_logits) {
+    if (!s) return fail(WH_ERR_INVALID, "seq: null handle");
+    WH_HIP(hipSetDevice(s->m->device));
+    int rc;
+    const float inv = temperature > 0 ? 1.0f / temperature : 1.0f;
+    if ((rc = set_sample_params_all(*s, inv, suppress_nst, nst))) return rc;
+    return step_greedy_impl(s, active, out_ids, out_logits);
 }
 
 // Up to n greedy steps of stream 0 with the reference's stop rules
@@ -709,7 +758,8 @@ int seq_step_topk(wh_seq *s, const int32_t *active, int32_t k, float temperature
     const int V = s->m->n_vocab;
     // the penalised copy `cur` is produced by the same pass that feeds greedy
     // selection; its argmax partials are unused here
-    if ((rc = launch_penalty_argmax(s->logits, s->hist, s->hist_len, s->hist_cap, s->active, s->S, V, inv, s->m->eot,
+    if ((rc = set_sample_params_all(*s, inv, 0, 0.0f))) return rc;
+    if ((rc = launch_penalty_argmax(s->logits, s->hist, s->hist_len, s->hist_cap, s->active, s->S, V, s->m->eot,
                                     s->sb, s->st)))
         return rc;
     // one extra candidate exposes a tie at the k-th place
@@ -848,8 +898,13 @@ int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, 
                         const wh_decode_params *params, int32_t *out_tokens, int32_t cap, int32_t *out_lens,
                         const volatile int32_t *cancel) {
     int rc;
-    for (int i = 0; i < S; i++)
+    for (int i = 0; i < S; i++) {
         if ((rc = check_params(*m, &params[i]))) return rc;
+        if (params[i].beam_size > 1)
+            return fail(WH_ERR_UNSUPPORTED, "model: decode: the stream batch decodes greedily; stream " +
+                                                std::to_string(i) + " asks for beam size " +
+                                                std::to_string(params[i].beam_size));
+    }
     wh_seq *sp = nullptr;
     if ((rc = seq_create(m, S, encs, enc_len, enc_dim, 0, &sp))) return rc;
     std::unique_ptr<wh_seq, void (*)(wh_seq *)> s(sp, seq_destroy);
@@ -863,7 +918,17 @@ int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, 
         if ((int)toks[i].size() >= p.prompt_len + maxt[i]) active[i] = 0;
         else if (p.prompt_len == 0) return fail(WH_ERR_INVALID, "model: decode: forward: no tokens in state");
     }
-    // one temperature / suppress setting per call: streams share the first params
+    // each stream samples with its own temperature (0 => 1.0, decoder.go:416-419),
+    // SuppressNST and NoSpeechThold
+    std::vector<float> inv(S), nst(S);
+    std::vector<int32_t> supp(S);
+    for (int i = 0; i < S; i++) {
+        const float base = params[i].temperature == 0 ? 1.0f : params[i].temperature;
+        inv[i] = base > 0 ? 1.0f / base : 1.0f;
+        supp[i] = params[i].suppress_nst;
+        nst[i] = params[i].no_speech_thold;
+    }
+    if ((rc = set_sample_params(*s, inv.data(), supp.data(), nst.data()))) return rc;
     const wh_decode_params &p0 = params[0];
     const float base = p0.temperature == 0 ? 1.0f : p0.temperature;
     if (S == 1 && active[0]) {
@@ -884,7 +949,7 @@ int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, 
     }
     while (std::any_of(active.begin(), active.end(), [](int32_t a) { return a != 0; })) {
         if (cancelled(cancel)) return fail(WH_ERR_CANCELLED, "model: decode: cancelled: context canceled");
-        if ((rc = seq_step_greedy(s.get(), active.data(), base, p0.suppress_nst, p0.no_speech_thold, ids.data(), nullptr)))
+        if ((rc = step_greedy_impl(s.get(), active.data(), ids.data(), nullptr)))
             return fail(rc, std::string("model: decode: forward: ") + wh_last_error());
         for (int i = 0; i < S; i++) {
             if (!active[i]) continue;
@@ -905,24 +970,31 @@ int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, 
     return WH_OK;
 }
 
-// decoder.go:528-726. The beam_size hypotheses run as one batch; every
-// hypothesis is reset before its forward (P9), the cross K/V are shared and
-// computed once (the reference recomputes identical values each step). The
-// bookkeeping runs on the device: top-k with log-normaliser (launch_topk, plus the
-// reference's scan for rows with ties), candidate ranking by normalised score
-// (a stable order among exact ties where Go's sort.Slice is unstable), the
-// prune and the next hypotheses' histories (k_beam_select). The host reads one
-// stop flag per step.
+// decoder.go:528-726. The beam_size hypotheses run as one batch of beam
+// objects (streams); every hypothesis is reset before its forward (P9), the cross
+// K/V are shared and computed once (the reference recomputes identical values
+// each step). The bookkeeping runs on the device: top-k with log-normaliser
+// (launch_topk, plus the reference's scan for rows with ties), candidate ranking
+// in Go's sort.Slice order, and the prune with the reference's in-place reuse of
+// the beam objects (k_beam_select). The host reads the stop words once per step.
 int decode_beam(const wh_model *m, const float *enc, int32_t enc_len, int32_t enc_dim, const wh_decode_params *p,
                 int32_t *out_tokens, int32_t cap, int32_t *out_len, const volatile int32_t *cancel) {
+    if (!p) return fail(WH_ERR_INVALID, "model: decode: null params");
+    if (p->prompt_len < 0 || (p->prompt_len > 0 && !p->prompt)) return fail(WH_ERR_INVALID, "model: decode: invalid prompt");
     int rc;
-    if ((rc = check_params(*m, p))) return rc;
     const float temp = p->temperature == 0 ? 1.0f : p->temperature;
     const float inv = temp > 0 ? 1.0f / temp : 1.0f;
-    const int bs = std::min(p->beam_size <= 0 ? 1 : p->beam_size, 16);
+    const int bs = p->beam_size <= 0 ? 1 : p->beam_size;
+    if (bs > 16)
+        return fail(WH_ERR_UNSUPPORTED, "model: decode: beam size " + std::to_string(bs) +
+                                            " exceeds the 16 hypotheses one batch holds");
     const int mt = cap_max_tokens(*m, *p);
     const int P = p->prompt_len;
     const int eot = m->eot;
+    // the forward embeds the last token (decoder.go:757-759); the penalty skips ids out of range
+    if (P > 0 && (p->prompt[P - 1] < 0 || p->prompt[P - 1] >= m->n_vocab) && mt > 0)
+        return fail(WH_ERR_INVALID, "model: decode: beam search forward: model: decode: forward: invalid token ID " +
+                                        std::to_string(p->prompt[P - 1]));
     if (mt <= 0 || (P > 0 && p->prompt[P - 1] == eot)) {
         // no step runs, or every hypothesis is finished from the start: the first is the prompt
         if (P > cap) return fail(WH_ERR_INVALID, "model: decode: output capacity too small");
@@ -930,40 +1002,49 @@ int decode_beam(const wh_model *m, const float *enc, int32_t enc_len, int32_t en
         *out_len = P;
         return WH_OK;
     }
-    if (P == 0) return fail(WH_ERR_INVALID, "model: decode: beam search forward: no tokens in state");
+    if (P == 0) return fail(WH_ERR_INVALID, "model: decode: beam search forward: model: decode: forward: no tokens in state");
     std::vector<const float *> encs(bs, enc);
     wh_seq *sp = nullptr;
     if ((rc = seq_create(m, bs, encs.data(), enc_len, enc_dim, 1, &sp))) return rc;
     std::unique_ptr<wh_seq, void (*)(wh_seq *)> s(sp, seq_destroy);
     wh_seq &q = *s;
-    const int hc = q.hist_cap, V = m->n_vocab, K = 5, KK = K + 1;
-    if (P + mt > hc) return fail(WH_ERR_INVALID, "model: decode: history capacity exceeded");
-    int32_t *hist_alt = nullptr, *len_alt = nullptr, *nbeams = nullptr, *stop = nullptr;
+    // a slot's history grows by at most one token per earlier slot of its step
+    const int hc = P + bs * (mt + 1) + 2, V = m->n_vocab, K = 5, KK = K + 1;
+    int32_t *hist = nullptr, *gcap = nullptr, *order = nullptr, *nbeams = nullptr, *stop = nullptr;
     float *score = nullptr, *powtab = nullptr;
-    if ((rc = q.alloc(&hist_alt, (size_t)bs * hc)) || (rc = q.alloc(&len_alt, (size_t)bs)) ||
-        (rc = q.alloc(&nbeams, 1)) || (rc = q.alloc(&stop, 1)) || (rc = q.alloc(&score, (size_t)bs)) ||
-        (rc = q.alloc(&powtab, (size_t)hc + 2)))
+    if ((rc = q.alloc(&hist, (size_t)bs * hc)) || (rc = q.alloc(&gcap, (size_t)bs)) ||
+        (rc = q.alloc(&order, (size_t)bs)) || (rc = q.alloc(&nbeams, 1)) || (rc = q.alloc(&stop, 4)) ||
+        (rc = q.alloc(&score, (size_t)bs)) || (rc = q.alloc(&powtab, (size_t)hc + 2)))
         return rc;
+    q.hist = hist;
+    q.hist_cap = hc;
     WH_HIP(hipSetDevice(m->device));
     {
-        // every hypothesis starts as the prompt with score 0; len^0.6 as the reference computes it
+        // every beam object starts as the prompt (capacity P) with score 0; len^0.6 as the reference computes it
         std::vector<float> pw((size_t)hc + 2);
         for (size_t n = 0; n < pw.size(); n++) pw[n] = (float)std::pow((double)n, 0.6);
-        std::vector<int32_t> h((size_t)bs * hc, 0), len(bs, P), tk(bs, p->prompt[P - 1]), ps(bs, P - 1), act(bs, 1);
-        for (int b = 0; b < bs; b++) std::memcpy(&h[(size_t)b * hc], p->prompt, sizeof(int32_t) * P);
+        std::vector<int32_t> h((size_t)bs * hc, 0), len(bs, P), tk(bs, p->prompt[P - 1]), ps(bs, P - 1), act(bs, 1),
+            ord(bs);
+        for (int b = 0; b < bs; b++) {
+            std::memcpy(&h[(size_t)b * hc], p->prompt, sizeof(int32_t) * P);
+            ord[b] = b;
+        }
         const std::vector<float> sc(bs, 0.0f);
-        const int32_t nb0 = bs, st0 = 0;
+        const int32_t nb0 = bs, st0[4] = {0, -1, 0, 0};
         WH_HIP(hipMemcpy(powtab, pw.data(), sizeof(float) * pw.size(), hipMemcpyHostToDevice));
         WH_HIP(hipMemcpy(q.hist, h.data(), sizeof(int32_t) * h.size(), hipMemcpyHostToDevice));
         WH_HIP(hipMemcpy(q.hist_len, len.data(), sizeof(int32_t) * bs, hipMemcpyHostToDevice));
+        WH_HIP(hipMemcpy(gcap, len.data(), sizeof(int32_t) * bs, hipMemcpyHostToDevice));
+        WH_HIP(hipMemcpy(order, ord.data(), sizeof(int32_t) * bs, hipMemcpyHostToDevice));
         WH_HIP(hipMemcpy(q.tok, tk.data(), sizeof(int32_t) * bs, hipMemcpyHostToDevice));
         WH_HIP(hipMemcpy(q.pos, ps.data(), sizeof(int32_t) * bs, hipMemcpyHostToDevice));
         WH_HIP(hipMemcpy(q.active, act.data(), sizeof(int32_t) * bs, hipMemcpyHostToDevice));
         WH_HIP(hipMemcpy(score, sc.data(), sizeof(float) * bs, hipMemcpyHostToDevice));
         WH_HIP(hipMemcpy(nbeams, &nb0, sizeof(int32_t), hipMemcpyHostToDevice));
-        WH_HIP(hipMemcpy(stop, &st0, sizeof(int32_t), hipMemcpyHostToDevice));
+        WH_HIP(hipMemcpy(stop, st0, sizeof(st0), hipMemcpyHostToDevice));
         for (int b = 0; b < bs; b++) q.h_active[b] = 1;  // host mirror: the profiler's byte counts only
     }
+    if ((rc = set_sample_params_all(q, inv, 0, 0.0f))) return rc;
     const int H = m->n_head, hd = m->n_state / H;
     for (int step = 0; step < mt; step++) {
         if (cancelled(cancel)) return fail(WH_ERR_CANCELLED, "model: decode: beam search cancelled: context canceled");
@@ -977,23 +1058,27 @@ int decode_beam(const wh_model *m, const float *enc, int32_t enc_len, int32_t en
         }
         WH_HIP(hipGetLastError());
         if ((rc = seq_forward(q)) ||
-            (rc = launch_penalty_argmax(q.logits, q.hist, q.hist_len, hc, q.active, bs, V, inv, eot, q.sb, q.st)) ||
+            (rc = launch_penalty_argmax(q.logits, q.hist, q.hist_len, hc, q.active, bs, V, eot, q.sb, q.st)) ||
             (rc = launch_topk(q.sb.cur, q.active, bs, V, KK, inv, q.topk_tok, q.topk_lp, q.topk_logz, q.topk_part, q.st)) ||
             (rc = launch_topk_ties(q.sb.cur, q.active, bs, V, K, KK, inv, q.topk_logz, q.topk_tok, q.topk_lp, q.st)) ||
-            (rc = launch_beam_select(q.topk_tok, q.topk_lp, K, KK, q.hist, q.hist_len, hist_alt, len_alt, hc, score,
-                                     nbeams, q.active, q.tok, q.pos, stop, powtab, bs, eot, q.st)))
+            (rc = launch_beam_select(q.topk_tok, q.topk_lp, K, KK, q.hist, q.hist_len, gcap, hc, score, order, nbeams,
+                                     q.active, q.tok, q.pos, stop, powtab, bs, eot, m->n_ctx, q.st)))
             return fail(rc, std::string("model: decode: beam search forward: ") + wh_last_error());
-        std::swap(q.hist, hist_alt);
-        std::swap(q.hist_len, len_alt);
-        WH_HIP(hipMemcpyAsync(q.pinned_ids, stop, sizeof(int32_t), hipMemcpyDeviceToHost, q.st));
+        WH_HIP(hipMemcpyAsync(q.pinned_ids, stop, sizeof(int32_t) * 3, hipMemcpyDeviceToHost, q.st));
         WH_HIP(hipStreamSynchronize(q.st));
         if (q.prof) q.prof_resolve();
+        if (q.pinned_ids[2]) return fail(WH_ERR_HIP, "model: decode: beam search: candidate sort stack exhausted");
         if (q.pinned_ids[0]) break;
+        if (q.pinned_ids[1] >= 0 && step + 1 < mt)
+            return fail(WH_ERR_INVALID, "model: decode: beam search forward: model: decode: forward: position " +
+                                            std::to_string(q.pinned_ids[1]) + " >= context length " +
+                                            std::to_string(m->n_ctx));
     }
-    int32_t len0 = 0;
-    WH_HIP(hipMemcpy(&len0, q.hist_len, sizeof(int32_t), hipMemcpyDeviceToHost));
+    int32_t o0 = 0, len0 = 0;
+    WH_HIP(hipMemcpy(&o0, order, sizeof(int32_t), hipMemcpyDeviceToHost));
+    WH_HIP(hipMemcpy(&len0, q.hist_len + o0, sizeof(int32_t), hipMemcpyDeviceToHost));
     if (len0 > cap) return fail(WH_ERR_INVALID, "model: decode: output capacity too small");
-    WH_HIP(hipMemcpy(out_tokens, q.hist, sizeof(int32_t) * len0, hipMemcpyDeviceToHost));
+    WH_HIP(hipMemcpy(out_tokens, q.hist + (size_t)o0 * hc, sizeof(int32_t) * len0, hipMemcpyDeviceToHost));
     *out_len = len0;
     return WH_OK;
 }

@@ -175,7 +175,8 @@ class HIPDecoder:
         """Full token sequence (prompt + generated) of Decode."""
         enc = self._check_enc(encoder_out)
         ps, keep = _params_struct(params)
-        cap = len(params.prompt) + self.n_ctx + 8
+        # a beam history grows by at most one token per hypothesis and step (in-place reuse)
+        cap = len(params.prompt) + max(1, int(params.beam_size)) * (self.n_ctx + 1) + 8
         out = (C.c_int32 * cap)()
         n = C.c_int32()
         cptr = C.pointer(cancel) if cancel is not None else None

@@ -100,6 +100,16 @@ def make_decoder(config="tiny.en", qtype=8, dims=None, std=0.02):
     return out, meta
 
 
+def stream_prompts(n_streams=16, seed=16, min_len=4, max_len=224):
+    """Prompts of the multi-stream workload: SOT/en/transcribe followed by ids
+    drawn from [0, 50000), total lengths uniform in [min_len, max_len]."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(min_len, max_len + 1, size=n_streams)
+    ids = rng.integers(0, 50000, size=(n_streams, max_len))
+    return [SOT_EN_TRANSCRIBE + [int(t) for t in ids[i, :lens[i] - len(SOT_EN_TRANSCRIBE)]]
+            for i in range(n_streams)]
+
+
 def encoder_output(config, d, stream=0, enc_len=ENC_LEN):
     """Synthetic encoder output [enc_len, d] ~ N(0, 1), seeded per stream."""
     return rng_for(config, f"encoder/{stream}").standard_normal((enc_len, d), dtype=np.float32)
@@ -145,15 +155,31 @@ def _gstr(s):
     return struct.pack("<Q", len(b)) + b
 
 
-def write_gguf(path, tensors, meta=None):
+_META_FMT = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<B", 10: "<Q", 11: "<q", 12: "<d"}
+
+
+def write_gguf(path, tensors, meta=None, extra=None):
     """Write tensors (+ uint32 whisper.* metadata) as GGUF v3
-    (internal/gguf/writer.go:24-107: 32-byte aligned header and tensors)."""
+    (internal/gguf/writer.go:24-107: 32-byte aligned header and tensors).
+    extra: further metadata as (key, gguf type code, value); type 8 is a string,
+    type 9 an array given as (element type, [values])."""
     kv = []
     keys = {"n_head": "whisper.decoder.attention.head_count", "n_layer": "whisper.decoder.layer_count",
             "n_ctx": "whisper.decoder.context_length", "n_state": "whisper.decoder.embedding_length",
             "n_vocab": "whisper.vocab.size"}
     for k, v in (meta or {}).items():
         kv.append(_gstr(keys[k]) + struct.pack("<II", 4, int(v)))
+
+    def value(t, v):
+        if t == 8:
+            return _gstr(v)
+        if t == 9:
+            et, vals = v
+            return struct.pack("<IQ", et, len(vals)) + b"".join(value(et, x) for x in vals)
+        return struct.pack(_META_FMT[t], v)
+
+    for k, t, v in (extra or []):
+        kv.append(_gstr(k) + struct.pack("<I", t) + value(t, v))
     infos, offsets, off = [], [], 0
     for t in tensors:
         offsets.append(off)
