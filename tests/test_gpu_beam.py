@@ -6,9 +6,12 @@ sort.Slice order (internal/model/decoder.go:575-718); the oracle restatement of
 both is pinned in tests/test_oracle_beam.py. Every case prints its name first,
 so a failing run names it.
 """
-import numpy as np
+import contextlib
+import os
+
 import pytest
 
+from conftest import rel_err
 from models import forced_repeat_model
 
 pytestmark = pytest.mark.gpu
@@ -160,4 +163,63 @@ def test_suppress_nst_greedy_vs_oracle(wh, orc, gpu, prompt):
     # without the suppression EOT ends the decode at once
     p.suppress_nst = False
     assert dec.decode_tokens(enc, p) == ref.decode(enc, p) == prompt + [T]
+    dec.close()
+
+
+@contextlib.contextmanager
+def batch_path(on):
+    """The batched persistent forward is chosen when a sequence is created (WHISPER_HIP_BATCH)."""
+    old = os.environ.get("WHISPER_HIP_BATCH")
+    os.environ["WHISPER_HIP_BATCH"] = "1" if on else "0"
+    try:
+        yield
+    finally:
+        if old is None:
+            del os.environ["WHISPER_HIP_BATCH"]
+        else:
+            os.environ["WHISPER_HIP_BATCH"] = old
+
+
+BATCH_MODELS = [
+    ("pb51", 7, (1200, 128, 2, 2, 48), 100),
+    ("pb80", 8, (2000, 192, 3, 2, 64), 300),
+    ("pb40", 2, (900, 128, 2, 1, 64), 1500),
+    ("pb41", 3, (1500, 256, 4, 2, 64), 513),
+    ("pb50", 6, (1000, 128, 2, 2, 64), 130),
+]
+
+
+@pytest.mark.parametrize("name,qtype,dims,enc_len", BATCH_MODELS)
+@pytest.mark.parametrize("S", [2, 5, 8])
+def test_batched_forward_vs_multikernel_and_oracle(wh, orc, gpu, name, qtype, dims, enc_len, S):
+    """The batched persistent forward (one launch per step for 2..8 states) gives
+    the multi-kernel path's logits (same arithmetic, another summation order) and
+    the oracle's, for states at position 0 (its own barrier) and past it."""
+    print(f"batched {name} S={S}", flush=True)
+    tensors, meta = wh.synth.make_decoder(name, qtype, dims=dims)
+    encs = [wh.synth.encoder_output(name, dims[1], stream=i, enc_len=enc_len) for i in range(S)]
+    dec = wh.HIPDecoder(tensors, meta)
+    ref = orc.OracleModel(tensors, meta)
+    prompts = [[1 + i] if i % 3 == 0 else list(range(2, 4 + i)) for i in range(S)]
+    seqs = {}
+    for on in (True, False):
+        with batch_path(on):
+            seqs[on] = dec.sequence(encs)
+        for i, p in enumerate(prompts):
+            seqs[on].set_tokens(i, p)
+    seqs[True].set_profiling(True)
+    states = [ref.state(p) for p in prompts]
+    for step in range(3):
+        ids_b, lg_b = seqs[True].step_greedy(logits=True)
+        ids_m, lg_m = seqs[False].step_greedy(logits=True)
+        for i in range(S):
+            want = states[i].forward(encs[i])
+            assert rel_err(lg_b[i], want) < 1e-3, (name, S, step, i)
+            assert rel_err(lg_b[i], lg_m[i]) < 2e-5, (name, S, step, i)
+            states[i].push(ids_b[i])
+        assert ids_b == ids_m, (name, S, step)
+    prof = seqs[True].profile()
+    assert prof.get("forward_batch", (0, 0, 0))[1] == 3, prof
+    for sq in seqs.values():
+        sq.close()
     dec.close()

@@ -17,7 +17,8 @@ LIBDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIBDIR, "libwhisper_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["wh_mega.hip", "wh_kernels.hip", "wh_seq.cpp", "wh_quant.cpp", "wh_model.cpp", "wh_api.cpp"]
+SOURCES = ["wh_mega.hip", "wh_kernels.hip", "wh_batch.hip", "wh_seq.cpp", "wh_quant.cpp", "wh_model.cpp",
+           "wh_api.cpp"]
 CFLAGS = [
     "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-x", "hip",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

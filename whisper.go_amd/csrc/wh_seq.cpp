@@ -10,12 +10,16 @@
 #include <string>
 #include <vector>
 
+#include "wh_batch.h"
 #include "wh_internal.h"
 #include "wh_mega.h"
 
 namespace wh {
 namespace mega {
 int launch_decode(uint32_t type, int grid, const MegaArgs &a, hipStream_t st);
+}
+namespace batch {
+int launch(uint32_t type, int grid, const BArgs &a, hipStream_t st);
 }
 
 __global__ void k_zero_rows(float *base, size_t stride, int count, int len) {
@@ -56,6 +60,15 @@ struct wh_seq {
     int64_t mega_launches = 0;
     wh::mega::MegaArgs mega{};
     int32_t *mega_state = nullptr;  // pinned host copy of state_out
+
+    // batched persistent forward (2..8 streams, reference mask, one quantised type)
+    bool batch_ok = false;
+    int batch_grid = 0;
+    uint32_t batch_type = 0;
+    int64_t batch_launches = 0;
+    wh::batch::BArgs bargs{};
+    unsigned *batch_errp = nullptr;  // pinned copy of the kernel's error word
+    bool batch_pending = false;      // a copy of it is queued since the last check
 
     // optional per-kernel timing: an event pair around every launch
     struct ProfCat {
@@ -106,6 +119,7 @@ struct wh_seq {
         for (void *p : allocs) (void)hipFree(p);
         if (pinned_ids) (void)hipHostFree(pinned_ids);
         if (mega_state) (void)hipHostFree(mega_state);
+        if (batch_errp) (void)hipHostFree(batch_errp);
         if (st) (void)hipStreamDestroy(st);
     }
     template <typename T>
@@ -150,7 +164,33 @@ struct Prof {
 
 double mat_bytes(const DevMat &m) { return (double)m.algo_bytes; }
 
+// One step's forward of every active stream in the batched persistent kernel.
+int batch_forward(wh_seq &s) {
+    int rc;
+    {
+        Prof p(s, "forward_batch", (double)s.m->weight_bytes);
+        if ((rc = batch::launch(s.batch_type, s.batch_grid, s.bargs, s.st))) return rc;
+    }
+    s.batch_launches++;
+    WH_HIP(hipMemcpyAsync(s.batch_errp, s.bargs.err, sizeof(unsigned), hipMemcpyDeviceToHost, s.st));
+    s.batch_pending = true;
+    return WH_OK;
+}
+
+// After the caller's stream synchronisation: a batched forward whose wait gave up
+// fails the step and turns the path off for this sequence.
+int batch_check(wh_seq &s) {
+    if (!s.batch_pending) return WH_OK;
+    s.batch_pending = false;
+    if (*s.batch_errp == 0) return WH_OK;
+    s.batch_ok = false;
+    (void)hipMemsetAsync(s.bargs.err, 0, sizeof(unsigned), s.st);
+    (void)hipStreamSynchronize(s.st);
+    return fail(WH_ERR_HIP, "batched persistent forward: a workgroup wait timed out");
+}
+
 int seq_forward(wh_seq &s) {
+    if (s.batch_ok && s.m->attn_mode == 0) return batch_forward(s);
     const wh_model &m = *s.m;
     const int S = s.S, d = m.n_state, H = m.n_head, hd = d / H, ctx = m.n_ctx;
     hipStream_t st = s.st;
@@ -391,6 +431,71 @@ int mega_setup(wh_seq &s) {
     return WH_OK;
 }
 
+// Set up the batched persistent forward for a sequence of 2..8 streams when the
+// model fits it (head size 64, width <= 2048, every matrix of the token
+// embedding's quantised type, q/k/v stacked); otherwise the multi-kernel chain
+// serves the steps.
+int batch_setup(wh_seq &s) {
+    const wh_model &m = *s.m;
+    s.batch_ok = false;
+    if (s.S < 2 || s.S > batch::SMAX || !env_int("WHISPER_HIP_BATCH", 1)) return WH_OK;
+    const int d = m.n_state, H = m.n_head, L = m.n_layer;
+    if (d / H != 64 || d % 64 != 0 || d > 2048 || !is_quant_type(m.tok.type)) return WH_OK;
+    for (const Layer &l : m.layers) {
+        if (!l.sqkv.alloc) return WH_OK;
+        const DevMat *ms[] = {&l.sqkv, &l.so, &l.cq, &l.co, &l.fc1, &l.fc2};
+        for (const DevMat *x : ms)
+            if (x->type != m.tok.type) return WH_OK;
+    }
+    int cus = 0, lds_max = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m.device) != hipSuccess) return WH_OK;
+    if (hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, m.device) != hipSuccess)
+        return WH_OK;
+    const int W = std::min(env_int("WHISPER_HIP_GRID", cus), cus);
+    // LDS for the staged [S][d] inputs; the fc2 column passes keep <= 16 rows per workgroup
+    if (W < 8 || (size_t)lds_max < batch::LDS_BYTES || (d + W - 1) / W > 16 ||
+        s.S * ((d + 31) / 32) > batch::XBUDGET / 128)
+        return WH_OK;
+    std::vector<batch::BLayer> ly(L);
+    for (int li = 0; li < L; li++) {
+        const Layer &l = m.layers[li];
+        batch::BLayer &x = ly[li];
+        x.sqkv = view(l.sqkv); x.so = view(l.so); x.cq = view(l.cq); x.co = view(l.co); x.fc1 = view(l.fc1);
+        x.fc2 = view(l.fc2);
+        x.ln1w = l.ln1w; x.ln1b = l.ln1b; x.svb = l.svb; x.sob = l.sob; x.ln2w = l.ln2w; x.ln2b = l.ln2b;
+        x.cqb = l.cqb; x.cob = l.cob; x.ln3w = l.ln3w; x.ln3b = l.ln3b; x.fc1b = l.fc1b; x.fc2b = l.fc2b;
+        x.kv = s.kv + (size_t)li * s.kv_layer;
+        x.kbase = s.kbase + (size_t)li * s.S;
+        x.vbase = s.vbase + (size_t)li * s.S;
+    }
+    int rc;
+    batch::BLayer *dl = nullptr;
+    if ((rc = s.alloc(&dl, (size_t)L))) return rc;
+    WH_HIP(hipMemcpy(dl, ly.data(), sizeof(batch::BLayer) * L, hipMemcpyHostToDevice));
+    batch::BArgs &a = s.bargs;
+    a.layers = dl;
+    a.L = L; a.d = d; a.H = H; a.ctx = m.n_ctx; a.V = m.n_vocab; a.enc_len = s.enc_len; a.S = s.S;
+    a.chunks = s.cb.chunks; a.chunk_len = s.cb.chunk_len;
+    a.kv_stream = s.kv_stream;
+    a.tok = view(m.tok);
+    a.pos_emb = m.pos; a.lnw = m.lnw; a.lnb = m.lnb;
+    a.tokv = s.tok; a.posv = s.pos; a.active = s.active;
+    a.x = s.x; a.q = s.q; a.attn = s.attn; a.h = s.h; a.logits = s.logits;
+    if ((rc = s.alloc(&a.x1, (size_t)s.S * d)) || (rc = s.alloc(&a.x2, (size_t)s.S * d))) return rc;
+    a.scores = s.cb.scores; a.cmax = s.cb.cmax; a.psum = s.cb.psum; a.pv = s.cb.pv;
+    if ((rc = s.alloc(&a.flags, (size_t)W)) || (rc = s.alloc(&a.err, 1))) return rc;
+    WH_HIP(hipMemsetAsync(a.flags, 0, sizeof(unsigned) * W, s.st));
+    WH_HIP(hipMemsetAsync(a.err, 0, sizeof(unsigned), s.st));
+    a.scale = (float)(1.0 / sqrt(64.0));
+    WH_HIP(hipHostMalloc((void **)&s.batch_errp, sizeof(unsigned), hipHostMallocDefault));
+    *s.batch_errp = 0;
+    WH_HIP(hipStreamSynchronize(s.st));
+    s.batch_grid = W;
+    s.batch_type = m.tok.type;
+    s.batch_ok = true;
+    return WH_OK;
+}
+
 // Run up to n greedy steps of stream 0 in the persistent kernel. Stops early on
 // the reference's rules when stop_rules is set (EOT, > 20 repeats, max_len).
 int mega_run(wh_seq &s, int n, float inv_temp, int suppress_nst, float nst, int max_len, int prev, int streak,
@@ -600,6 +705,7 @@ int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t e
     (void)hipFree(enc);
     WH_HIP(hipStreamSynchronize(s->st));
     if ((rc = mega_setup(*s))) return rc;
+    if ((rc = batch_setup(*s))) return rc;
     *out = s.release();
     return WH_OK;
 }
@@ -680,6 +786,7 @@ static int step_greedy_impl(wh_seq *s, const int32_t *active, int32_t *out_ids, 
     if (out_logits)
         WH_HIP(hipMemcpyAsync(out_logits, s->logits, sizeof(float) * (size_t)s->S * V, hipMemcpyDeviceToHost, s->st));
     WH_HIP(hipStreamSynchronize(s->st));
+    if ((rc = batch_check(*s))) return rc;
     if (s->prof) s->prof_resolve();
     for (int i = 0; i < s->S; i++) {
         if (out_ids) out_ids[i] = s->h_active[i] ? s->pinned_ids[i] : -1;
@@ -775,6 +882,7 @@ int seq_step_topk(wh_seq *s, const int32_t *active, int32_t k, float temperature
     if (out_logits)
         WH_HIP(hipMemcpyAsync(out_logits, s->logits, sizeof(float) * (size_t)s->S * V, hipMemcpyDeviceToHost, s->st));
     WH_HIP(hipStreamSynchronize(s->st));
+    if ((rc = batch_check(*s))) return rc;
     if (s->prof) s->prof_resolve();
     std::vector<float> row;
     for (int i = 0; i < s->S; i++) {
@@ -1066,6 +1174,7 @@ int decode_beam(const wh_model *m, const float *enc, int32_t enc_len, int32_t en
             return fail(rc, std::string("model: decode: beam search forward: ") + wh_last_error());
         WH_HIP(hipMemcpyAsync(q.pinned_ids, stop, sizeof(int32_t) * 3, hipMemcpyDeviceToHost, q.st));
         WH_HIP(hipStreamSynchronize(q.st));
+        if ((rc = batch_check(q))) return fail(rc, std::string("model: decode: beam search forward: ") + wh_last_error());
         if (q.prof) q.prof_resolve();
         if (q.pinned_ids[2]) return fail(WH_ERR_HIP, "model: decode: beam search: candidate sort stack exhausted");
         if (q.pinned_ids[0]) break;
