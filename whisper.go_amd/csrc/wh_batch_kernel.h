@@ -4,34 +4,44 @@
 //
 // The multi-kernel path runs a step as ~13 launches per layer; each launch costs
 // a dispatch and a drain of the whole chip. Here one workgroup per CU walks the
-// phases of the step and the phases meet at grid barriers:
-//   embed                x = token row + positional row                 (once)
-//   per layer l:
-//     A   LN1(x); q,k,v rows (k, v -> KV cache at pos); self-attention out rows
-//         on V cache row 0 (the reference mask attends row 0 only,
-//         internal/ml/attention.go:250-256): x1 = x + (Wo.V0 + bo). When a
-//         state is at position 0 its row 0 is written in this phase, so the
-//         out rows then wait for a barrier of their own.
-//     B   LN2(x1); cross query rows -> q
-//     C   cross scores of (state, head, key chunk) items, chunk maxima
-//     D   fast-exp weights against the head maximum, partial P.V per chunk
-//     E   head combine -> attn
-//     F   cross out rows: x2 = x1 + (Wo_c.attn + b)
-//     G   LN3(x2); fc1 rows + GELU -> h
-//     H   fc2 rows: x = x2 + (W2.h + b2)
-//   final LN; tied logits rows -> logits
-// Each phase splits the rows of its matrix evenly over the workgroups; a
-// workgroup stages the phase's input activations of all S states in LDS once
-// (LayerNorm computed on the way, one wave per state) and every decoded weight
-// block feeds the S states. The arithmetic is that of the multi-kernel kernels
-// (exact integer codes, fp32 FMA accumulation, LayerNorm in two passes with a
-// float64 sqrt, GELU with a float64 tanh, the reference's fast exp); only the
-// summation order differs.
+// phases of the step and the phases meet at grid barriers.
 //
-// Barrier: every workgroup releases its stores at agent scope, publishes its
-// phase number, and waits until all workgroups have published it, then
-// acquires. Every wait is bounded: on expiry the error word is set, later waits
-// return at once, and the host reports a failure.
+// Under the reference mask a state past position 0 attends KV row 0 only
+// (internal/ml/attention.go:250-256), so its self-attention output
+// sa_l = Wo_l . V0_l + bo_l depends on no activation of the step: all layers'
+// sa_l are computed in the first phase, together with the embedding. A layer is
+// then six phases:
+//   B   LN1(x) -> k,v rows into the KV cache at pos (two thirds of the
+//       workgroups); LN2(x + sa_l) -> cross query rows (the other third)
+//   C   cross scores of (state, head, key chunk) items and chunk maxima
+//   D   fast-exp weights against the head maximum, partial P.V per chunk; the
+//       last chunk of a head to finish combines the head -> attn
+//   F   cross out rows: x2 = (x + sa_l) + (Wo_c.attn + b)
+//   G   LN3(x2); fc1 rows + GELU -> h
+//   H   fc2 rows: x = x2 + (W2.h + b2)
+// and the step ends with the final LN and the tied logits rows. When a state is
+// at position 0 its V0_l is written within the step, so each layer runs the k,v
+// rows, the sa_l rows and the query rows as three phases instead.
+//
+// Each GEMV phase splits the rows of its matrix evenly over the workgroups; a
+// workgroup stages the phase's input activations of all S states in LDS once
+// (LayerNorm computed on the way) and every decoded weight block feeds the S
+// states. The arithmetic is that of the multi-kernel kernels (exact integer
+// codes, fp32 FMA accumulation, LayerNorm in two passes with a float64 sqrt, GELU
+// with a float64 tanh, the reference's fast exp); only the summation order
+// differs.
+//
+// Exchange between workgroups: every value another workgroup reads within the
+// launch is stored and loaded with relaxed agent-scope atomics, which bypass
+// the per-XCD caches, so the barrier needs no cache writeback or invalidation:
+// each wave waits for its stores to complete, the workgroup publishes its phase
+// number and waits until all workgroups have published it. Every wait is
+// bounded: on expiry the error word is set, later waits return at once, and the
+// host reports a failure.
+#pragma once
+// Included by the per-format sources wh_batch_q*.hip, each of which
+// instantiates the kernel for one weight type (the instantiations compile in
+// parallel).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -46,7 +56,7 @@ namespace batch {
 constexpr int NWV = NT / 64;
 constexpr int XBLK = XBUDGET / 128;  // staged 32-float blocks, over all states
 constexpr unsigned SPIN_MAX = 1u << 22;
-constexpr int CHUNK = 128;           // keys per cross-attention item
+constexpr int RW = 4;                // rows per lane group and pass
 
 // ---- cross-lane sums ---------------------------------------------------------------
 __device__ __forceinline__ float wsum(float v) {
@@ -59,15 +69,61 @@ __device__ __forceinline__ float wmax(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
 }
+// sum over aligned groups of G lanes
+template <int G>
+__device__ __forceinline__ float gsum(float v) {
+#pragma unroll
+    for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// ---- global memory ---------------------------------------------------------------------
+// Pointers read from descriptors are generic; typed as global memory, their loads
+// are global_load (vector memory counter only) instead of flat_load, which would
+// also hold up every LDS wait.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const float gcf;
+typedef __attribute__((address_space(1))) const f32x4 gcf4;
+typedef __attribute__((address_space(1))) const u32x4 gcu4;
+typedef __attribute__((address_space(1))) const uint16_t gcu16;
+typedef __attribute__((address_space(1))) const uint32_t gcu32;
+typedef __attribute__((address_space(1))) const uint64_t gcu64;
+typedef __attribute__((address_space(1))) uint32_t gu32;
+typedef __attribute__((address_space(1))) float gf;
+
+__device__ __forceinline__ float ldg(const float *p) { return *(gcf *)p; }
+__device__ __forceinline__ float4 ldg4(const float *p) {
+    const f32x4 v = *(gcf4 *)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void stg(float *p, float v) { *(gf *)p = v; }
+
+// ---- exchanged values ----------------------------------------------------------------
+__device__ __forceinline__ float ldx(const float *p) {
+    return __uint_as_float(__hip_atomic_load((gcu32 *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+// four consecutive floats at a 16-byte aligned address
+__device__ __forceinline__ float4 ldx4(const float *p) {
+    const uint64_t a = __hip_atomic_load((gcu64 *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t b = __hip_atomic_load((gcu64 *)p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float4(__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)),
+                       __uint_as_float((uint32_t)b), __uint_as_float((uint32_t)(b >> 32)));
+}
+__device__ __forceinline__ void stx(float *p, float v) {
+    __hip_atomic_store((gu32 *)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// this wave's stores (and loads) have completed
+__device__ __forceinline__ void stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ---- grid barrier -------------------------------------------------------------------
 __device__ __forceinline__ bool failed(unsigned *err) {
     return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
 
-__device__ void gbar(unsigned *flags, unsigned *err, unsigned &g) {
+__device__ __forceinline__ void gbar(unsigned *flags, unsigned *err, unsigned &g) {
     ++g;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    stores_done();
     __syncthreads();
     if (threadIdx.x < 64) {
         if (threadIdx.x == 0) __hip_atomic_store(flags + blockIdx.x, g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -84,7 +140,6 @@ __device__ void gbar(unsigned *flags, unsigned *err, unsigned &g) {
         }
     }
     __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 }
 
 // ---- weight blocks ------------------------------------------------------------------
@@ -96,17 +151,19 @@ struct Blk {
 template <int TYPE>
 __device__ __forceinline__ void blk_load(const MatView &m, size_t blk, Blk &r) {
     if constexpr (TYPE == 8) {
-        const uint4 *p = (const uint4 *)(m.qs + blk * 32);
-        r.a = p[0];
-        r.b = p[1];
-        r.s = ((const uint16_t *)m.sc)[blk];
+        gcu4 *p = (gcu4 *)(m.qs + blk * 32);
+        const u32x4 a = p[0], b = p[1];
+        r.a = make_uint4(a.x, a.y, a.z, a.w);
+        r.b = make_uint4(b.x, b.y, b.z, b.w);
+        r.s = ((gcu16 *)m.sc)[blk];
         r.h = 0u;
     } else {
-        r.a = *(const uint4 *)(m.qs + blk * 16);
+        const u32x4 a = *(gcu4 *)(m.qs + blk * 16);
+        r.a = make_uint4(a.x, a.y, a.z, a.w);
         r.b = make_uint4(0u, 0u, 0u, 0u);
-        if constexpr (TYPE == 3 || TYPE == 7) r.s = ((const uint32_t *)m.sc)[blk];
-        else r.s = ((const uint16_t *)m.sc)[blk];
-        if constexpr (TYPE == 6 || TYPE == 7) r.h = m.qh[blk];
+        if constexpr (TYPE == 3 || TYPE == 7) r.s = ((gcu32 *)m.sc)[blk];
+        else r.s = ((gcu16 *)m.sc)[blk];
+        if constexpr (TYPE == 6 || TYPE == 7) r.h = ((gcu32 *)m.qh)[blk];
         else r.h = 0u;
     }
 }
@@ -148,7 +205,15 @@ __device__ __forceinline__ float bscale(const Blk &r, float qx, float sx) {
     else return __builtin_fmaf(h2f(r.s & 0xFFFFu), qx, h2f(r.s >> 16) * sx);
 }
 
-// ---- staged activations in LDS -------------------------------------------------------
+// ---- LDS --------------------------------------------------------------------------------
+struct Lds {
+    float4 *xs;   // staged blocks
+    float *sx;    // their sums
+    float *lw, *lb;  // LayerNorm weight and bias
+    int *pos;     // [SMAX] positions
+    float *red;   // reduction area (1024 floats)
+};
+
 // State s, block b (of nbc staged blocks), chunk k (elements 4k..4k+3) at float4
 // slot (s * nbc + b) * 8 + ((k + b) & 7): the lanes of a wave read consecutive
 // blocks at one k and hit distinct banks. Block sums (4/5-bit formats) at
@@ -156,7 +221,7 @@ __device__ __forceinline__ float bscale(const Blk &r, float qx, float sx) {
 __device__ __forceinline__ int slot(int s, int nbc, int b, int k) { return (s * nbc + b) * 8 + ((k + b) & 7); }
 
 // Block sums of the staged blocks, in the order the multi-kernel GEMV uses.
-__device__ void stage_sums(int S, int nbc, const float4 *xs, float *sx) {
+__device__ __forceinline__ void stage_sums(int S, int nbc, const float4 *xs, float *sx) {
     for (int i = threadIdx.x; i < S * nbc; i += NT) {
         const int s = i / nbc, b = i % nbc;
         float t = 0.0f;
@@ -169,19 +234,38 @@ __device__ void stage_sums(int S, int nbc, const float4 *xs, float *sx) {
     }
 }
 
-// Blocks [c0, c0 + nbc) of rows src(s, col) of the S states (zero past cols).
+// Columns [32 c0, 32 (c0 + nbc)) of the S states' rows into the staged layout:
+// src(s, col) gives elements col..col+3 (col a multiple of 4; zero past cols).
+// Eight loads per thread are in flight before the first LDS store.
 template <class Src>
-__device__ void stage_cols(int S, int cols, int c0, int nbc, Src src, float4 *xs, float *sx, bool sums) {
-    for (int i = threadIdx.x; i < S * nbc * 8; i += NT) {
-        const int s = i / (nbc * 8), r = i % (nbc * 8), b = r >> 3, k = r & 7;
-        const int col = (c0 + b) * 32 + 4 * k;
-        float4 v;
-        v.x = col < cols ? src(s, col) : 0.0f;
-        v.y = col + 1 < cols ? src(s, col + 1) : 0.0f;
-        v.z = col + 2 < cols ? src(s, col + 2) : 0.0f;
-        v.w = col + 3 < cols ? src(s, col + 3) : 0.0f;
-        xs[slot(s, nbc, b, k)] = v;
+__device__ __forceinline__ void burst(int S, int cols, int c0, int nbc, Src src, float4 *xs) {
+    const int n = S * nbc * 8;
+    for (int i0 = threadIdx.x; i0 < n; i0 += NT * 8) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = i0 + u * NT;
+            v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (i < n) {
+                const int s = i / (nbc * 8), r = i % (nbc * 8);
+                const int col = (c0 + (r >> 3)) * 32 + 4 * (r & 7);
+                if (col < cols) v[u] = src(s, col);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = i0 + u * NT;
+            if (i < n) {
+                const int s = i / (nbc * 8), r = i % (nbc * 8);
+                xs[slot(s, nbc, r >> 3, r & 7)] = v[u];
+            }
+        }
     }
+}
+
+template <class Src>
+__device__ __forceinline__ void stage_cols(int S, int cols, int c0, int nbc, Src src, float4 *xs, float *sx, bool sums) {
+    burst(S, cols, c0, nbc, src, xs);
     __syncthreads();
     if (sums) {
         stage_sums(S, nbc, xs, sx);
@@ -189,55 +273,74 @@ __device__ void stage_cols(int S, int cols, int c0, int nbc, Src src, float4 *xs
     }
 }
 
-// LayerNorm (internal/ml/ops.go:153-202) of the d-element rows x[s] of the S
-// states into the staged layout, one wave per state: the mean, then the mean of
-// squared deviations, std = float32(sqrt(float64(var + eps))), w*(x-mean)/std + b.
-// A lane keeps its elements (lane + 64 j) in their LDS slots between the passes.
-__device__ void stage_ln(int S, int d, const float *x, const float *w, const float *bb, float4 *xs, float *sx,
-                         bool sums) {
+// LayerNorm (internal/ml/ops.go:153-202) of the d-element rows src(s, .) of the
+// S states into the staged layout: the mean, then the mean of squared
+// deviations, std = float32(sqrt(float64(var + eps))), w*(x-mean)/std + b. The
+// rows and the weights are loaded in one burst; the statistics take one wave per
+// state, in LDS.
+template <class Src>
+__device__ __forceinline__ void stage_ln(int S, int d, Src src, const float *w, const float *bb, const Lds &L, bool sums) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int nbc = (d + 31) / 32;
-    float *xf = (float *)xs;
-    for (int s = wv; s < S; s += NWV) {
-        const float *xr = x + (size_t)s * d;
-        float t = 0.0f;
-        for (int i = lane; i < nbc * 32; i += 64) {
-            const float v = i < d ? xr[i] : 0.0f;  // the tail of the last block stays zero
-            xf[slot(s, nbc, i >> 5, (i & 31) >> 2) * 4 + (i & 3)] = v;
-            t += v;
+    const int nbc = d / 32, dq = d / 4;
+    float4 wr[2], br[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int i = min((int)threadIdx.x + u * NT, dq - 1);
+        wr[u] = ldg4(w + 4 * i);
+        br[u] = ldg4(bb + 4 * i);
+    }
+    burst(S, d, 0, nbc, src, L.xs);
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int i = threadIdx.x + u * NT;
+        if (i < dq) {
+            ((float4 *)L.lw)[i] = wr[u];
+            ((float4 *)L.lb)[i] = br[u];
         }
+    }
+    __syncthreads();
+    float *xf = (float *)L.xs;
+    for (int s = wv; s < S; s += NWV) {
+        float t = 0.0f;
+#pragma unroll 8
+        for (int i = lane; i < d; i += 64) t += xf[slot(s, nbc, i >> 5, (i & 31) >> 2) * 4 + (i & 3)];
         const float mean = wsum(t) / (float)d;
         float q = 0.0f;
+#pragma unroll 8
         for (int i = lane; i < d; i += 64) {
             const float u = xf[slot(s, nbc, i >> 5, (i & 31) >> 2) * 4 + (i & 3)] - mean;
             q += u * u;
         }
         const float var = wsum(q) / (float)d;
         const float sd = (float)sqrt((double)(var + 1e-5f));
+#pragma unroll 8
         for (int i = lane; i < d; i += 64) {
             float &e = xf[slot(s, nbc, i >> 5, (i & 31) >> 2) * 4 + (i & 3)];
-            e = w[i] * (e - mean) / sd + bb[i];
+            e = L.lw[i] * (e - mean) / sd + L.lb[i];
         }
     }
     __syncthreads();
     if (sums) {
-        stage_sums(S, nbc, xs, sx);
+        stage_sums(S, nbc, L.xs, L.sx);
         __syncthreads();
     }
 }
 
 // ---- GEMV over a row range, all states at once ----------------------------------------
-// Rows [rg, rg + RW) of w (clamped to row1 - 1; the extra rows' results are
-// dropped), staged blocks [0, nbc) = matrix blocks [c0, c0 + nbc): lane l takes
-// blocks l, l + 64, ...; every decoded chunk of codes feeds the S states.
-template <int TYPE, int RW>
+// Lanes form groups of G: lane l works on row rg + r * (64 / G) + l / G (r < RW,
+// clamped to row1 - 1; the extra rows' results are dropped) and takes staged
+// blocks l % G, l % G + G, ... of [0, nbc) = matrix blocks [c0, c0 + nbc); every
+// decoded chunk of codes feeds the S states.
+template <int TYPE, int G>
 __device__ __forceinline__ void dots(const MatView &w, int rg, int row1, int S, int c0, int nbc, const float4 *xs,
                                      const float *sx, float (&acc)[RW][SMAX]) {
-    const int lane = threadIdx.x & 63;
-    for (int b = lane; b < nbc; b += 64) {
+    constexpr int RPS = 64 / G;
+    const int lane = threadIdx.x & 63, ro = lane / G;
+    for (int b = lane % G; b < nbc; b += G) {
         Blk rb[RW];
 #pragma unroll
-        for (int r = 0; r < RW; r++) blk_load<TYPE>(w, (size_t)min(rg + r, row1 - 1) * w.nb + c0 + b, rb[r]);
+        for (int r = 0; r < RW; r++)
+            blk_load<TYPE>(w, (size_t)min(rg + r * RPS + ro, row1 - 1) * w.nb + c0 + b, rb[r]);
         float qx[RW][SMAX];
 #pragma unroll
         for (int r = 0; r < RW; r++)
@@ -282,41 +385,70 @@ __device__ __forceinline__ void dots(const MatView &w, int rg, int row1, int S, 
     }
 }
 
-template <int RW, class Epi>
-__device__ __forceinline__ void finish(int rg, int row1, int S, const int32_t *active, float (&acc)[RW][SMAX],
-                                       Epi epi) {
-    const int lane = threadIdx.x & 63;
+// The epilogue operands pre(s, row) of the lane's rows, loaded before the dot
+// products so that their latency overlaps the weight loads.
+template <int G, class Pre>
+__device__ __forceinline__ void load_pre(int rg, int row1, int S, Pre pre, float2 (&ad)[RW][SMAX]) {
+    constexpr int RPS = 64 / G;
+    const int ro = (threadIdx.x & 63) / G;
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        const int row = min(rg + r * RPS + ro, row1 - 1);
+#pragma unroll
+        for (int s = 0; s < SMAX; s++) ad[r][s] = s < S ? pre(s, row) : make_float2(0.f, 0.f);
+    }
+}
+
+template <int G, class Epi>
+__device__ __forceinline__ void finish(int rg, int row1, int S, unsigned amask, float (&acc)[RW][SMAX],
+                                       const float2 (&ad)[RW][SMAX], Epi epi) {
+    constexpr int RPS = 64 / G;
+    const int lane = threadIdx.x & 63, ro = lane / G;
 #pragma unroll
     for (int r = 0; r < RW; r++)
 #pragma unroll
         for (int s = 0; s < SMAX; s++)
             if (s < S) {
-                const float v = wsum(acc[r][s]);
-                if (lane == 0 && rg + r < row1 && active[s]) epi(s, rg + r, v);
+                const float v = gsum<G>(acc[r][s]);
+                const int row = rg + r * RPS + ro;
+                if (lane % G == 0 && row < row1 && ((amask >> s) & 1u)) epi(s, row, v, ad[r][s]);
             }
 }
 
 // Rows [row0, row1) of w against the staged input (already in LDS when `staged`,
-// else staged here from src in passes of as many blocks as fit).
-template <int TYPE, int RW, class Src, class Epi>
-__device__ void gemv(const MatView &w, int row0, int row1, int S, const int32_t *active, bool staged, Src src,
-                     float4 *xs, float *sx, Epi epi) {
+// else staged here from src in passes of as many blocks as fit). A workgroup
+// without rows returns at once (uniformly).
+template <int TYPE, int G, class Src, class Pre, class Epi>
+__device__ __forceinline__ void gemv(const MatView &w, int row0, int row1, int S, unsigned amask, bool staged, Src src,
+                                     const Lds &L, Pre pre, Epi epi) {
+    gemv_g<TYPE, G>(w, row0, row1, S, amask, staged, src, L, pre, epi);
+}
+
+template <int TYPE, int G, class Src, class Pre, class Epi>
+__device__ __forceinline__ void gemv_g(const MatView &w, int row0, int row1, int S, unsigned amask, bool staged, Src src,
+                       const Lds &L, Pre pre, Epi epi) {
+    if (row0 >= row1) return;
+    constexpr int WR = RW * (64 / G);  // rows of a wave's pass
     const int wv = threadIdx.x >> 6, nb = w.nb, per = XBLK / S;
     if (staged || nb <= per) {
-        if (!staged) stage_cols(S, w.cols, 0, nb, src, xs, sx, TYPE != 8);
-        for (int rg = row0 + wv * RW; rg < row1; rg += NWV * RW) {
+        if (!staged) stage_cols(S, w.cols, 0, nb, src, L.xs, L.sx, TYPE != 8);
+        for (int rg = row0 + wv * WR; rg < row1; rg += NWV * WR) {
+            float2 ad[RW][SMAX];
+            load_pre<G>(rg, row1, S, pre, ad);
             float acc[RW][SMAX];
 #pragma unroll
             for (int r = 0; r < RW; r++)
 #pragma unroll
                 for (int s = 0; s < SMAX; s++) acc[r][s] = 0.0f;
-            dots<TYPE, RW>(w, rg, row1, S, 0, nb, xs, sx, acc);
-            finish<RW>(rg, row1, S, active, acc, epi);
+            dots<TYPE, G>(w, rg, row1, S, 0, nb, L.xs, L.sx, acc);
+            finish<G>(rg, row1, S, amask, acc, ad, epi);
         }
     } else {
-        // passes over the columns; each wave keeps its RW rows' sums across the passes
-        // (the host sizes the grid so a workgroup has at most NWV * RW rows here)
-        const int rg = row0 + wv * RW;
+        // passes over the columns; each wave keeps its rows' sums across the passes
+        // (the host sizes the grid so a workgroup has at most NWV * WR rows here)
+        const int rg = row0 + wv * WR;
+        float2 ad[RW][SMAX];
+        load_pre<G>(rg, row1, S, pre, ad);
         float acc[RW][SMAX];
 #pragma unroll
         for (int r = 0; r < RW; r++)
@@ -324,137 +456,202 @@ __device__ void gemv(const MatView &w, int row0, int row1, int S, const int32_t 
             for (int s = 0; s < SMAX; s++) acc[r][s] = 0.0f;
         for (int c0 = 0; c0 < nb; c0 += per) {
             const int nbc = min(per, nb - c0);
-            stage_cols(S, w.cols, c0, nbc, src, xs, sx, TYPE != 8);
-            if (rg < row1) dots<TYPE, RW>(w, rg, row1, S, c0, nbc, xs, sx, acc);
+            stage_cols(S, w.cols, c0, nbc, src, L.xs, L.sx, TYPE != 8);
+            if (rg < row1) dots<TYPE, G>(w, rg, row1, S, c0, nbc, L.xs, L.sx, acc);
             __syncthreads();
         }
-        if (rg < row1) finish<RW>(rg, row1, S, active, acc, epi);
+        if (rg < row1) finish<G>(rg, row1, S, amask, acc, ad, epi);
     }
     __syncthreads();
 }
 
+
 __device__ __forceinline__ int split(int n, int w, int W) { return (int)((long)n * w / W); }
 
 // ---- the step ------------------------------------------------------------------------------
-template <int TYPE>
+// G: lanes per row group, 32 for models of width <= 1024, else 64
+template <int TYPE, int G>
 __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
     extern __shared__ float4 lds4[];
-    float4 *xs = lds4;
-    float *sx = (float *)(lds4 + XBLK * 8);
-    float *red = sx + XBLK;  // reduction area (1024 floats)
+    Lds L;
+    L.xs = lds4;
+    L.sx = (float *)(lds4 + XBLK * 8);
+    L.lw = L.sx + XBLK;
+    L.lb = L.lw + LNMAX;
+    L.pos = (int *)(L.lb + LNMAX);
+    L.red = (float *)(L.pos + 64);
+    BLayer *lyl = (BLayer *)(L.red + 1024);  // the layer descriptors, copied once
     const int W = (int)gridDim.x, w = (int)blockIdx.x;
-    const int S = a.S, d = a.d, H = a.H, L = a.L, C = a.chunks;
+    const int S = a.S, d = a.d, H = a.H, Ln = a.L, C = a.chunks;
+    {
+        const int n = Ln * (int)(sizeof(BLayer) / 8);
+        for (int i = threadIdx.x; i < n; i += NT) ((uint64_t *)lyl)[i] = ((gcu64 *)a.layers)[i];
+    }
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     // the phase counter continues from this workgroup's last published phase (every
     // workgroup passes the same barriers, so all start from the same value)
     unsigned *const flags = a.flags, *const errw = a.err;
     unsigned g = __hip_atomic_load(flags + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned amask = 0;
     bool pos0 = false;
-    for (int s = 0; s < S; s++) pos0 |= a.active[s] && a.posv[s] == 0;
+    for (int s = 0; s < S; s++) {
+        const bool on = a.active[s] != 0;
+        amask |= (unsigned)on << s;
+        pos0 |= on && a.posv[s] == 0;
+    }
+    if (threadIdx.x < S) L.pos[threadIdx.x] = a.posv[threadIdx.x];
+    __syncthreads();
+
+    const int ctx = a.ctx, enc_len = a.enc_len;
+    const size_t kvs = a.kv_stream, plane = (size_t)H * ctx * 64;
+    float *xg = a.x, *x2g = a.x2, *qg = a.q, *attng = a.attn, *hg = a.h, *sag = a.sa;
+    const int *posl = L.pos;
+    const auto nosrc = [](int, int) { return make_float4(0.f, 0.f, 0.f, 0.f); };
+    const auto nopre = [](int, int) { return make_float2(0.f, 0.f); };
+    // rows of this layer's self-attention output sa_l = Wo V0 + bo (V0: KV row 0)
+    const auto sa_rows = [&](const BLayer *ly, float *sal, int r0, int r1) __attribute__((always_inline)) {
+        const float *vp = ly->kv + plane;
+        const float *sob = ly->sob;
+        gemv<TYPE, G>(
+            ly->so, r0, r1, S, amask, false,
+            [=](int s, int c) { return ldx4(vp + (size_t)s * kvs + (size_t)(c >> 6) * ctx * 64 + (c & 63)); }, L,
+            [=](int, int r) { return make_float2(0.f, ldg(sob + r)); },
+            [=](int s, int r, float v, float2 p) { stx(sal + (size_t)s * d + r, v + p.y); });
+    };
+    // k,v rows [d + r0, d + r1) of the stacked q,k,v matrix into the KV cache at pos
+    const auto kv_rows = [&](const BLayer *ly, int r0, int r1) __attribute__((always_inline)) {
+        if (r0 >= r1) return;
+        const float *xr = xg;
+        stage_ln(S, d, [=](int s, int c) { return ldx4(xr + (size_t)s * d + c); }, ly->ln1w, ly->ln1b, L,
+                 TYPE != 8);
+        float *kv = ly->kv;
+        const float *svb = ly->svb;
+        gemv<TYPE, G>(ly->sqkv, d + r0, d + r1, S, amask, true, nosrc, L,
+                   [=](int, int r) { return make_float2(0.f, r >= 2 * d ? ldg(svb + r - 2 * d) : 0.0f); },
+                   [=](int s, int r, float v, float2 p) {
+                       const int j = r % d;
+                       stx(kv + (size_t)s * kvs + (r >= 2 * d ? plane : 0) + (size_t)(j >> 6) * ctx * 64 +
+                               (size_t)posl[s] * 64 + (j & 63),
+                           v + p.y);
+                   });
+    };
+    // cross query rows [r0, r1) from LN2(x + sa_l)
+    const auto cq_rows = [&](const BLayer *ly, const float *sal, int r0, int r1) __attribute__((always_inline)) {
+        if (r0 >= r1) return;
+        const float *xr = xg;
+        stage_ln(
+            S, d,
+            [=](int s, int c) {
+                const float4 u = ldx4(xr + (size_t)s * d + c), v = ldx4(sal + (size_t)s * d + c);
+                return make_float4(u.x + v.x, u.y + v.y, u.z + v.z, u.w + v.w);
+            },
+            ly->ln2w, ly->ln2b, L, TYPE != 8);
+        const float *cqb = ly->cqb;
+        float *qw = qg;
+        gemv<TYPE, G>(ly->cq, r0, r1, S, amask, true, nosrc, L, [=](int, int r) { return make_float2(0.f, ldg(cqb + r)); },
+                   [=](int s, int r, float v, float2 p) { stx(qw + (size_t)s * d + r, v + p.y); });
+    };
 
     // embedding (decoder.go:756-773): the quantised row is dequantised bit-exactly
     for (int i = split(S * d, w, W) + threadIdx.x; i < split(S * d, w + 1, W); i += NT) {
         const int s = i / d, e = i % d;
-        if (!a.active[s]) continue;
-        a.x[i] = dequant_elem<TYPE>(a.tok, a.tokv[s], e >> 5, e & 31) + a.pos_emb[(size_t)a.posv[s] * d + e];
+        if (!((amask >> s) & 1u)) continue;
+        stx(xg + i, dequant_elem<TYPE>(a.tok, a.tokv[s], e >> 5, e & 31) + ldg(a.pos_emb + (size_t)posl[s] * d + e));
+    }
+    // past position 0 every layer's sa_l is known now: its rows for all layers
+    if (!pos0) {
+        const int r0 = split(Ln * d, w, W), r1 = split(Ln * d, w + 1, W);
+        for (int l = r0 / d; l < Ln && l * d < r1; l++)
+            sa_rows(lyl + l, sag + (size_t)l * S * d, max(r0, l * d) - l * d, min(r1, (l + 1) * d) - l * d);
     }
     gbar(flags, errw, g);
 
     // after a failed wait every barrier returns at once: the launch runs out and the
     // host reports the failure
-    const int32_t *act = a.active, *posv = a.posv;
-    float *xg = a.x, *x1g = a.x1, *x2g = a.x2, *qg = a.q, *attng = a.attn, *hg = a.h;
-    const int ctx = a.ctx, enc_len = a.enc_len;
-    const size_t kvs = a.kv_stream, plane = (size_t)H * ctx * 64;
-    for (int l = 0; l < L; l++) {
-        const BLayer *ly = a.layers + l;
-        // ---- A: LN1, q,k,v rows; self-attention out rows on V row 0 ----
-        stage_ln(S, d, xg, ly->ln1w, ly->ln1b, xs, sx, TYPE != 8);
-        {
-            float *kv = ly->kv;
-            const float *svb = ly->svb;
-            gemv<TYPE, 2>(ly->sqkv, split(3 * d, w, W), split(3 * d, w + 1, W), S, act, true,
-                          [](int, int) { return 0.0f; }, xs, sx, [=](int s, int r, float v) {
-                              // rows [0,d) q (unread under the reference mask), [d,2d) k, [2d,3d) v + b
-                              if (r < d) return;
-                              const int j = r % d;
-                              float *dst = kv + (size_t)s * kvs + (r >= 2 * d ? plane : 0) +
-                                           (size_t)(j >> 6) * ctx * 64 + (size_t)posv[s] * 64 + (j & 63);
-                              *dst = r >= 2 * d ? v + svb[j] : v;
-                          });
-        }
-        if (pos0) gbar(flags, errw, g);  // a state at position 0 attends the row it just wrote
-        {
-            const float *vp = ly->kv + plane;
-            const float *sob = ly->sob;
-            gemv<TYPE, 2>(ly->so, split(d, w, W), split(d, w + 1, W), S, act, false,
-                          [=](int s, int c) { return vp[(size_t)s * kvs + (size_t)(c >> 6) * ctx * 64 + (c & 63)]; },
-                          xs, sx, [=](int s, int r, float v) {
-                              x1g[(size_t)s * d + r] = xg[(size_t)s * d + r] + (v + sob[r]);
-                          });
-        }
-        gbar(flags, errw, g);
-        // ---- B: LN2, cross query rows ----
-        stage_ln(S, d, x1g, ly->ln2w, ly->ln2b, xs, sx, TYPE != 8);
-        {
-            const float *cqb = ly->cqb;
-            gemv<TYPE, 2>(ly->cq, split(d, w, W), split(d, w + 1, W), S, act, true, [](int, int) { return 0.0f; },
-                          xs, sx, [=](int s, int r, float v) { qg[(size_t)s * d + r] = v + cqb[r]; });
+    const int Wk = W - W / 3;  // k,v workgroups of phase B
+    for (int l = 0; l < Ln; l++) {
+        const BLayer *ly = lyl + l;
+        float *sal = sag + (size_t)l * S * d;
+        // ---- B: k,v rows; cross query rows ----
+        if (pos0) {
+            kv_rows(ly, split(2 * d, w, W), split(2 * d, w + 1, W));
+            gbar(flags, errw, g);
+            sa_rows(ly, sal, split(d, w, W), split(d, w + 1, W));
+            gbar(flags, errw, g);
+            cq_rows(ly, sal, split(d, w, W), split(d, w + 1, W));
+        } else if (w < Wk) {
+            kv_rows(ly, split(2 * d, w, Wk), split(2 * d, w + 1, Wk));
+        } else {
+            cq_rows(ly, sal, split(d, w - Wk, W - Wk), split(d, w + 1 - Wk, W - Wk));
         }
         gbar(flags, errw, g);
         // ---- C: scores of (state, head, chunk) items and chunk maxima ----
         for (int it = w; it < S * H * C; it += W) {
             const int s = it / (H * C), h = (it / C) % H, c = it % C;
-            if (!act[s]) continue;
-            const int slot16 = lane & 15;
-            const float4 q4 = ((const float4 *)(qg + (size_t)s * d + h * 64))[slot16];
-            const float *K = ly->kbase[s] + (size_t)h * enc_len * 64;
+            if (!((amask >> s) & 1u)) continue;
+            const int q16 = lane & 15;
+            const float4 q4 = ldx4(qg + (size_t)s * d + h * 64 + q16 * 4);
+            const float *K = (const float *)((gcu64 *)ly->kbase)[s] + (size_t)h * enc_len * 64;
             const int t0 = c * CHUNK, t1 = min(t0 + CHUNK, enc_len);
+            float4 k4[CHUNK / 16];
+#pragma unroll
+            for (int j = 0; j < CHUNK / 16; j++) {
+                const int t = t0 + j * 16 + wv * 4 + (lane >> 4);
+                k4[j] = t < t1 ? ldg4(K + (size_t)t * 64 + q16 * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
             float mx = -INFINITY;
-            for (int t = t0 + wv * 4 + (lane >> 4); t - (lane >> 4) < t1; t += 4 * NWV) {
-                float part = 0.0f;
-                if (t < t1) {
-                    const float4 k4 = ((const float4 *)(K + (size_t)t * 64))[slot16];
-                    part = q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
-                }
-                float dot = part;
+#pragma unroll
+            for (int j = 0; j < CHUNK / 16; j++) {
+                const int t = t0 + j * 16 + wv * 4 + (lane >> 4);
+                float dot = q4.x * k4[j].x + q4.y * k4[j].y + q4.z * k4[j].z + q4.w * k4[j].w;
 #pragma unroll
                 for (int o = 8; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 64);
                 if (t < t1) {
                     const float sco = dot * a.scale;
-                    if (slot16 == 0) a.scores[((size_t)s * H + h) * enc_len + t] = sco;
+                    if (q16 == 0) stx(a.scores + ((size_t)s * H + h) * enc_len + t, sco);
                     mx = fmaxf(mx, sco);
                 }
             }
             mx = wmax(mx);
-            if (lane == 0) red[wv] = mx;
+            if (lane == 0) L.red[wv] = mx;
             __syncthreads();
             if (threadIdx.x == 0) {
-                float m = red[0];
-                for (int i = 1; i < NWV; i++) m = fmaxf(m, red[i]);
-                a.cmax[((size_t)s * H + h) * C + c] = m;
+                float m = L.red[0];
+                for (int i = 1; i < NWV; i++) m = fmaxf(m, L.red[i]);
+                stx(a.cmax + it, m);
             }
             __syncthreads();
         }
         gbar(flags, errw, g);
-        // ---- D: fast-exp weights against the head maximum, partial P.V ----
+        // ---- D: fast-exp weights against the head maximum, partial P.V; head combine ----
         for (int it = w; it < S * H * C; it += W) {
             const int s = it / (H * C), h = (it / C) % H, c = it % C;
-            if (!act[s]) continue;
-            const int slot16 = lane & 15;
-            float M = -INFINITY;
-            const float *cm = a.cmax + ((size_t)s * H + h) * C;
-            for (int i = 0; i < C; i++) M = fmaxf(M, cm[i]);
-            const float *V = ly->vbase[s] + (size_t)h * enc_len * 64;
-            const float *sc = a.scores + ((size_t)s * H + h) * enc_len;
+            if (!((amask >> s) & 1u)) continue;
+            const int q16 = lane & 15;
+            const size_t sh = (size_t)s * H + h;
+            float M = lane < C ? ldx(a.cmax + sh * C + lane) : -INFINITY;
+            const float *V = (const float *)((gcu64 *)ly->vbase)[s] + (size_t)h * enc_len * 64;
+            const float *sc = a.scores + sh * enc_len;
             const int t0 = c * CHUNK, t1 = min(t0 + CHUNK, enc_len);
+            float sv[CHUNK / 16];
+            float4 v4[CHUNK / 16];
+#pragma unroll
+            for (int j = 0; j < CHUNK / 16; j++) {
+                const int t = t0 + j * 16 + wv * 4 + (lane >> 4);
+                sv[j] = t < t1 ? ldx(sc + t) : 0.0f;
+                v4[j] = t < t1 ? ldg4(V + (size_t)t * 64 + q16 * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            M = wmax(M);
             float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
             float es = 0.0f;
-            for (int t = t0 + wv * 4 + (lane >> 4); t < t1; t += 4 * NWV) {
-                const float e = fast_exp(sc[t] - M);
-                const float4 v4 = ((const float4 *)(V + (size_t)t * 64))[slot16];
-                acc.x += e * v4.x; acc.y += e * v4.y; acc.z += e * v4.z; acc.w += e * v4.w;
-                if (slot16 == 0) es += e;
+#pragma unroll
+            for (int j = 0; j < CHUNK / 16; j++) {
+                const int t = t0 + j * 16 + wv * 4 + (lane >> 4);
+                if (t < t1) {
+                    const float e = fast_exp(sv[j] - M);
+                    acc.x += e * v4[j].x; acc.y += e * v4[j].y; acc.z += e * v4[j].z; acc.w += e * v4[j].w;
+                    if (q16 == 0) es += e;
+                }
             }
 #pragma unroll
             for (int o = 16; o < 64; o <<= 1) {
@@ -464,93 +661,106 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
                 acc.w += __shfl_xor(acc.w, o, 64);
             }
             es = wsum(es);
-            float4 *red4 = (float4 *)red;  // [NWV][16]
+            float4 *red4 = (float4 *)L.red;  // [NWV][16]
             if (lane < 16) red4[wv * 16 + lane] = acc;
-            if (lane == 0) red[512 + wv] = es;
+            if (lane == 0) L.red[512 + wv] = es;
             __syncthreads();
-            const size_t item = ((size_t)s * H + h) * C + c;
             if (threadIdx.x < 16) {
                 float4 r = red4[threadIdx.x];
                 for (int i = 1; i < NWV; i++) {
                     const float4 t4 = red4[i * 16 + threadIdx.x];
                     r.x += t4.x; r.y += t4.y; r.z += t4.z; r.w += t4.w;
                 }
-                ((float4 *)(a.pv + item * 64))[threadIdx.x] = r;
+                float *dst = a.pv + (size_t)it * 64 + threadIdx.x * 4;
+                stx(dst, r.x); stx(dst + 1, r.y); stx(dst + 2, r.z); stx(dst + 3, r.w);
             }
             if (threadIdx.x == 0) {
                 float t = 0.0f;
-                for (int i = 0; i < NWV; i++) t += red[512 + i];
-                a.psum[item] = t;
+                for (int i = 0; i < NWV; i++) t += L.red[512 + i];
+                stx(a.psum + it, t);
+            }
+            // the last chunk of the head to get here combines the head's chunks
+            stores_done();
+            __syncthreads();
+            int *last = (int *)(L.red + 520);
+            if (threadIdx.x == 0)
+                *last = __hip_atomic_fetch_add(a.heads + sh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                        (unsigned)(C - 1);
+            __syncthreads();
+            if (*last && threadIdx.x < 64) {
+                const float ps = lane < C ? ldx(a.psum + sh * C + lane) : 0.0f;
+                float o = 0.0f;
+#pragma unroll 4
+                for (int i = 0; i < C; i++) o += ldx(a.pv + (sh * C + i) * 64 + lane);
+                const float sum = wsum(ps);
+                stx(attng + (size_t)s * d + h * 64 + lane, o * (1.0f / sum));
+                if (lane == 0) __hip_atomic_store(a.heads + sh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
             __syncthreads();
         }
         gbar(flags, errw, g);
-        // ---- E: head combine, one wave per (state, head) ----
-        for (int it = w * NWV + wv; it < S * H; it += W * NWV) {
-            const int s = it / H, h = it % H;
-            if (!act[s]) continue;
-            const float *ps = a.psum + (size_t)it * C;
-            float sum = 0.0f;
-            for (int i = 0; i < C; i++) sum += ps[i];
-            float o = 0.0f;
-            for (int i = 0; i < C; i++) o += a.pv[((size_t)it * C + i) * 64 + lane];
-            attng[(size_t)s * d + h * 64 + lane] = o * (1.0f / sum);
-        }
-        gbar(flags, errw, g);
-        // ---- F: cross out rows ----
+        // ---- F: cross out rows; x2 = (x + sa_l) + (Wo_c.attn + b) ----
         {
-            const float *cob = ly->cob;
-            gemv<TYPE, 2>(ly->co, split(d, w, W), split(d, w + 1, W), S, act, false,
-                          [=](int s, int c) { return attng[(size_t)s * d + c]; }, xs, sx, [=](int s, int r, float v) {
-                              x2g[(size_t)s * d + r] = x1g[(size_t)s * d + r] + (v + cob[r]);
-                          });
+            const float *cob = ly->cob, *xr = xg, *ar = attng;
+            float *x2w = x2g;
+            gemv<TYPE, G>(
+                ly->co, split(d, w, W), split(d, w + 1, W), S, amask, false,
+                [=](int s, int c) { return ldx4(ar + (size_t)s * d + c); }, L,
+                [=](int s, int r) {
+                    return make_float2(ldx(xr + (size_t)s * d + r) + ldx(sal + (size_t)s * d + r), ldg(cob + r));
+                },
+                [=](int s, int r, float v, float2 p) { stx(x2w + (size_t)s * d + r, p.x + (v + p.y)); });
         }
         gbar(flags, errw, g);
         // ---- G: LN3, fc1 rows + GELU ----
-        stage_ln(S, d, x2g, ly->ln3w, ly->ln3b, xs, sx, TYPE != 8);
         {
-            const float *fc1b = ly->fc1b;
-            gemv<TYPE, 2>(ly->fc1, split(4 * d, w, W), split(4 * d, w + 1, W), S, act, true,
-                          [](int, int) { return 0.0f; }, xs, sx,
-                          [=](int s, int r, float v) { hg[(size_t)s * 4 * d + r] = gelu_ref(v + fc1b[r]); });
+            const int r0 = split(4 * d, w, W), r1 = split(4 * d, w + 1, W);
+            if (r0 < r1) {
+                const float *x2r = x2g, *fc1b = ly->fc1b;
+                float *hw = hg;
+                stage_ln(S, d, [=](int s, int c) { return ldx4(x2r + (size_t)s * d + c); }, ly->ln3w, ly->ln3b, L,
+                         TYPE != 8);
+                gemv<TYPE, G>(ly->fc1, r0, r1, S, amask, true, nosrc, L,
+                           [=](int, int r) { return make_float2(0.f, ldg(fc1b + r)); },
+                           [=](int s, int r, float v, float2 p) { stx(hw + (size_t)s * 4 * d + r, gelu_ref(v + p.y)); });
+            }
         }
         gbar(flags, errw, g);
-        // ---- H: fc2 rows ----
+        // ---- H: fc2 rows; x = x2 + (W2.h + b2) ----
         {
-            const float *fc2b = ly->fc2b;
-            gemv<TYPE, 2>(ly->fc2, split(d, w, W), split(d, w + 1, W), S, act, false,
-                          [=](int s, int c) { return hg[(size_t)s * 4 * d + c]; }, xs, sx, [=](int s, int r, float v) {
-                              xg[(size_t)s * d + r] = x2g[(size_t)s * d + r] + (v + fc2b[r]);
-                          });
+            const float *fc2b = ly->fc2b, *hr = hg, *x2r = x2g;
+            float *xw = xg;
+            gemv<TYPE, G>(
+                ly->fc2, split(d, w, W), split(d, w + 1, W), S, amask, false,
+                [=](int s, int c) { return ldx4(hr + (size_t)s * 4 * d + c); }, L,
+                [=](int s, int r) { return make_float2(ldx(x2r + (size_t)s * d + r), ldg(fc2b + r)); },
+                [=](int s, int r, float v, float2 p) { stx(xw + (size_t)s * d + r, p.x + (v + p.y)); });
         }
         gbar(flags, errw, g);
     }
     // ---- final LayerNorm and tied logits rows (decoder.go:817-832) ----
-    stage_ln(S, d, xg, a.lnw, a.lnb, xs, sx, TYPE != 8);
     {
-        float *lg = a.logits;
-        const int V = a.V;
-        gemv<TYPE, 2>(a.tok, split(V, w, W), split(V, w + 1, W), S, act, true, [](int, int) { return 0.0f; }, xs, sx,
-                      [=](int s, int r, float v) { lg[(size_t)s * V + r] = v; });
+        const int r0 = split(a.V, w, W), r1 = split(a.V, w + 1, W);
+        if (r0 < r1) {
+            const float *xr = xg;
+            float *lg = a.logits;
+            const int V = a.V;
+            stage_ln(S, d, [=](int s, int c) { return ldx4(xr + (size_t)s * d + c); }, a.lnw, a.lnb, L, TYPE != 8);
+            gemv<TYPE, G>(a.tok, r0, r1, S, amask, true, nosrc, L, nopre,
+                       [=](int s, int r, float v, float2) { stg(lg + (size_t)s * V + r, v); });
+        }
     }
 }
 
-int launch(uint32_t type, int grid, const BArgs &a, hipStream_t st) {
+// Launch of the kernel for weight type TYPE; G from the model width.
+template <int TYPE>
+int launch_type(int grid, const BArgs &a, hipStream_t st) {
     void *args[] = {(void *)&a};
-    const void *fn = nullptr;
-    switch (type) {
-    case 2: fn = (const void *)k_fwd_batch<2>; break;
-    case 3: fn = (const void *)k_fwd_batch<3>; break;
-    case 6: fn = (const void *)k_fwd_batch<6>; break;
-    case 7: fn = (const void *)k_fwd_batch<7>; break;
-    case 8: fn = (const void *)k_fwd_batch<8>; break;
-    default: return fail(WH_ERR_UNSUPPORTED, "batched persistent forward: unsupported weight type");
-    }
+    const void *fn = a.d <= 1024 ? (const void *)k_fwd_batch<TYPE, 32> : (const void *)k_fwd_batch<TYPE, 64>;
     WH_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BYTES));
     WH_HIP(hipLaunchCooperativeKernel(fn, dim3(grid), dim3(NT), args, LDS_BYTES, st));
     return WH_OK;
 }
-
 
 }  // namespace batch
 }  // namespace wh

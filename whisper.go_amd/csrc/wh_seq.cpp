@@ -431,14 +431,15 @@ int mega_setup(wh_seq &s) {
     return WH_OK;
 }
 
-// Set up the batched persistent forward for a sequence of 2..8 streams when the
-// model fits it (head size 64, width <= 2048, every matrix of the token
-// embedding's quantised type, q/k/v stacked); otherwise the multi-kernel chain
-// serves the steps.
+// Set up the batched persistent forward for a sequence of 2..8 streams when it
+// is asked for (WHISPER_HIP_BATCH=1; until it outruns the multi-kernel chain it
+// is not the default) and the model fits it (head size 64, width <= 2048, every
+// matrix of the token embedding's quantised type, q/k/v stacked); otherwise the
+// multi-kernel chain serves the steps.
 int batch_setup(wh_seq &s) {
     const wh_model &m = *s.m;
     s.batch_ok = false;
-    if (s.S < 2 || s.S > batch::SMAX || !env_int("WHISPER_HIP_BATCH", 1)) return WH_OK;
+    if (s.S < 2 || s.S > batch::SMAX || !env_int("WHISPER_HIP_BATCH", 0)) return WH_OK;
     const int d = m.n_state, H = m.n_head, L = m.n_layer;
     if (d / H != 64 || d % 64 != 0 || d > 2048 || !is_quant_type(m.tok.type)) return WH_OK;
     for (const Layer &l : m.layers) {
@@ -452,9 +453,10 @@ int batch_setup(wh_seq &s) {
     if (hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, m.device) != hipSuccess)
         return WH_OK;
     const int W = std::min(env_int("WHISPER_HIP_GRID", cus), cus);
-    // LDS for the staged [S][d] inputs; the fc2 column passes keep <= 16 rows per workgroup
-    if (W < 8 || (size_t)lds_max < batch::LDS_BYTES || (d + W - 1) / W > 16 ||
-        s.S * ((d + 31) / 32) > batch::XBUDGET / 128)
+    // LDS for the staged [S][d] inputs and the LayerNorm weights; the fc2 column
+    // passes keep <= 16 rows per workgroup; a head has at most CMAX key chunks
+    if (W < 8 || (size_t)lds_max < batch::LDS_BYTES || (d + W - 1) / W > 16 || d > batch::LNMAX || L > batch::LMAX ||
+        s.S * (d / 32) > batch::XBUDGET / 128 || s.cb.chunks > batch::CMAX)
         return WH_OK;
     std::vector<batch::BLayer> ly(L);
     for (int li = 0; li < L; li++) {
@@ -475,15 +477,18 @@ int batch_setup(wh_seq &s) {
     batch::BArgs &a = s.bargs;
     a.layers = dl;
     a.L = L; a.d = d; a.H = H; a.ctx = m.n_ctx; a.V = m.n_vocab; a.enc_len = s.enc_len; a.S = s.S;
-    a.chunks = s.cb.chunks; a.chunk_len = s.cb.chunk_len;
+    a.chunks = s.cb.chunks;
     a.kv_stream = s.kv_stream;
     a.tok = view(m.tok);
     a.pos_emb = m.pos; a.lnw = m.lnw; a.lnb = m.lnb;
     a.tokv = s.tok; a.posv = s.pos; a.active = s.active;
     a.x = s.x; a.q = s.q; a.attn = s.attn; a.h = s.h; a.logits = s.logits;
-    if ((rc = s.alloc(&a.x1, (size_t)s.S * d)) || (rc = s.alloc(&a.x2, (size_t)s.S * d))) return rc;
+    if ((rc = s.alloc(&a.x2, (size_t)s.S * d)) || (rc = s.alloc(&a.sa, (size_t)L * s.S * d))) return rc;
     a.scores = s.cb.scores; a.cmax = s.cb.cmax; a.psum = s.cb.psum; a.pv = s.cb.pv;
-    if ((rc = s.alloc(&a.flags, (size_t)W)) || (rc = s.alloc(&a.err, 1))) return rc;
+    if ((rc = s.alloc(&a.heads, (size_t)s.S * H)) || (rc = s.alloc(&a.flags, (size_t)W)) ||
+        (rc = s.alloc(&a.err, 1)))
+        return rc;
+    WH_HIP(hipMemsetAsync(a.heads, 0, sizeof(unsigned) * s.S * H, s.st));
     WH_HIP(hipMemsetAsync(a.flags, 0, sizeof(unsigned) * W, s.st));
     WH_HIP(hipMemsetAsync(a.err, 0, sizeof(unsigned), s.st));
     a.scale = (float)(1.0 / sqrt(64.0));
