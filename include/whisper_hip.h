@@ -85,6 +85,13 @@ float wh_f16_to_f32(uint16_t h);
  * kernels use, copies the float32 result back. Replaces gguf.Dequantize
  * (internal/gguf/dequant.go:47-85) for types 0,1,2,3,6,7,8. */
 int wh_dequantize(uint32_t type, const void *raw, uint64_t nbytes, uint64_t n, float *out, int32_t device);
+/* wh_dequantize without any device allocation: no counterpart in the
+ * reference; it is for callers that cannot allocate (serving loops, harnesses
+ * that forbid hipMalloc). The raw blocks, their device layout and the result
+ * are staged in a 16 MiB device array the library holds on each device until
+ * the process ends; n is at most 1048576 (WH_ERR_INVALID beyond). Calls that
+ * overlap on one device race on that array. Same results, bit for bit. */
+int wh_dequantize_noalloc(uint32_t type, const void *raw, uint64_t nbytes, uint64_t n, float *out, int32_t device);
 
 /* ---- standalone quantised GEMV ------------------------------------------- */
 /* A device-resident quantised matrix [rows, cols] (row-major GGUF blocks per

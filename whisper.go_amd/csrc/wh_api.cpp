@@ -263,6 +263,10 @@ int wh_dequantize(uint32_t type, const void *raw, uint64_t nbytes, uint64_t n, f
     return rc;
 }
 
+int wh_dequantize_noalloc(uint32_t type, const void *raw, uint64_t nbytes, uint64_t n, float *out, int32_t device) {
+    return dequantize_noalloc(type, raw, nbytes, n, out, device);
+}
+
 int wh_matrix_create(uint32_t type, int32_t rows, int32_t cols, const void *raw, uint64_t nbytes, int32_t device,
                      wh_matrix **out) {
     if (!out || !raw) return fail(WH_ERR_INVALID, "NewQuantizedMatrix: null argument");

@@ -118,6 +118,8 @@ struct GemvIn {
 int launch_gemv(const DevMat *const *mats, const GemvIn *in, const GemvOut *out, int nmat, int batch,
                 hipStream_t st);
 int launch_dequant_rows(const DevMat &m, int32_t row0, int32_t nrows, float *out, hipStream_t st);
+// wh_dequantize with every staging buffer in a file-scope device array (wh_noalloc.hip).
+int dequantize_noalloc(uint32_t type, const void *raw, uint64_t nbytes, uint64_t n, float *out, int32_t device);
 
 struct SeqDev;  // defined in wh_seq.cpp
 int launch_embed(const wh_model &m, const int32_t *tok, const int32_t *pos, const int32_t *active, float *x,
