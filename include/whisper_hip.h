@@ -185,6 +185,12 @@ int wh_decode_batch(const wh_model *m, int32_t n_streams, const float *const *en
                     int32_t enc_dim, const wh_decode_params *params, int32_t *out_tokens, int32_t cap,
                     int32_t *out_lens, const volatile int32_t *cancel);
 
+/* *out = forward steps (token-loop iterations) of the calling thread's last
+ * wh_decode / wh_decode_batch call. Under the reference's beam search a
+ * hypothesis may grow by more than one token per step, so its length does not
+ * tell the step count. No counterpart in the reference: benchmarks read it. */
+int wh_last_decode_steps(int32_t *out);
+
 /* ---- step-level sequence API (one decoder state per stream) ---------------- */
 /* A batch of decoder states with persistent KV caches and cached cross-attention
  * K/V in HBM; replaces decoderState (internal/model/decoder.go:306-386).

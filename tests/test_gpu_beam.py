@@ -223,3 +223,18 @@ def test_batched_forward_vs_multikernel_and_oracle(wh, orc, gpu, name, qtype, di
     for sq in seqs.values():
         sq.close()
     dec.close()
+
+
+def test_last_decode_steps(wh, orc, gpu):
+    """wh_last_decode_steps counts token-loop iterations: for greedy decoding the
+    generated tokens, for beam search the steps even where the best hypothesis
+    grew by more than one token per step."""
+    dec, ref, enc = _setup(wh, orc, *BEAM_MODELS[0])
+    p = wh.DecoderParams(prompt=[5, 6, 7], max_tokens=9, no_fallback=True)
+    got = dec.decode_tokens(enc, p)
+    assert dec.last_decode_steps() == len(got) - 3 == 9
+    p = wh.DecoderParams(prompt=[5, 6, 7], beam_size=5, max_tokens=12, no_fallback=True)
+    got = dec.decode_tokens(enc, p)
+    assert got == ref.decode(enc, p)
+    assert dec.last_decode_steps() == 12
+    dec.close()

@@ -41,6 +41,7 @@ int seq_profile_get(wh_seq *s, int32_t i, char *name, int32_t cap, double *ms, i
 int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, int32_t enc_len, int32_t enc_dim,
                         const wh_decode_params *params, int32_t *out_tokens, int32_t cap, int32_t *out_lens,
                         const volatile int32_t *cancel);
+int32_t last_decode_steps();
 int decode_beam(const wh_model *m, const float *enc, int32_t enc_len, int32_t enc_dim, const wh_decode_params *p,
                 int32_t *out_tokens, int32_t cap, int32_t *out_len, const volatile int32_t *cancel);
 
@@ -337,6 +338,12 @@ int wh_model_weight_bytes(const wh_model *m, uint64_t *bytes) {
 int wh_model_set_attention_mode(wh_model *m, int32_t mode) {
     if (!m || (mode != 0 && mode != 1)) return fail(WH_ERR_INVALID, "attention mode must be 0 or 1");
     m->attn_mode = mode;
+    return WH_OK;
+}
+
+int wh_last_decode_steps(int32_t *out) {
+    if (!out) return fail(WH_ERR_INVALID, "null argument");
+    *out = last_decode_steps();
     return WH_OK;
 }
 

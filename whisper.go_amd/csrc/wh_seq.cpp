@@ -1007,10 +1007,15 @@ bool cancelled(const volatile int32_t *c) { return c && *c != 0; }
 
 // decoder.go:413-525 for n_streams independent streams (no vocabulary: no
 // compression-ratio retries).
+// Forward steps of the calling thread's last decode (wh_last_decode_steps).
+thread_local int32_t g_decode_steps = 0;
+int32_t last_decode_steps() { return g_decode_steps; }
+
 int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, int32_t enc_len, int32_t enc_dim,
                         const wh_decode_params *params, int32_t *out_tokens, int32_t cap, int32_t *out_lens,
                         const volatile int32_t *cancel) {
     int rc;
+    g_decode_steps = 0;
     for (int i = 0; i < S; i++) {
         if ((rc = check_params(*m, &params[i]))) return rc;
         if (params[i].beam_size > 1)
@@ -1057,6 +1062,7 @@ int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, 
                                     pv, st)))
                 return fail(rc, std::string("model: decode: forward: ") + wh_last_error());
             toks[0].insert(toks[0].end(), got.begin(), got.begin() + n);
+            g_decode_steps += n;
             if (n < CHUNK || toks[0].back() == m->eot || st > 20 || (int)toks[0].size() >= max_len) active[0] = 0;
         }
     }
@@ -1064,6 +1070,7 @@ int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, 
         if (cancelled(cancel)) return fail(WH_ERR_CANCELLED, "model: decode: cancelled: context canceled");
         if ((rc = step_greedy_impl(s.get(), active.data(), ids.data(), nullptr)))
             return fail(rc, std::string("model: decode: forward: ") + wh_last_error());
+        g_decode_steps++;
         for (int i = 0; i < S; i++) {
             if (!active[i]) continue;
             const int32_t next = ids[i];
@@ -1095,6 +1102,7 @@ int decode_beam(const wh_model *m, const float *enc, int32_t enc_len, int32_t en
     if (!p) return fail(WH_ERR_INVALID, "model: decode: null params");
     if (p->prompt_len < 0 || (p->prompt_len > 0 && !p->prompt)) return fail(WH_ERR_INVALID, "model: decode: invalid prompt");
     int rc;
+    g_decode_steps = 0;
     const float temp = p->temperature == 0 ? 1.0f : p->temperature;
     const float inv = temp > 0 ? 1.0f / temp : 1.0f;
     const int bs = p->beam_size <= 0 ? 1 : p->beam_size;
@@ -1179,6 +1187,7 @@ int decode_beam(const wh_model *m, const float *enc, int32_t enc_len, int32_t en
             return fail(rc, std::string("model: decode: beam search forward: ") + wh_last_error());
         WH_HIP(hipMemcpyAsync(q.pinned_ids, stop, sizeof(int32_t) * 3, hipMemcpyDeviceToHost, q.st));
         WH_HIP(hipStreamSynchronize(q.st));
+        g_decode_steps++;
         if ((rc = batch_check(q))) return fail(rc, std::string("model: decode: beam search forward: ") + wh_last_error());
         if (q.prof) q.prof_resolve();
         if (q.pinned_ids[2]) return fail(WH_ERR_HIP, "model: decode: beam search: candidate sort stack exhausted");

@@ -186,6 +186,14 @@ class HIPDecoder:
             _raise(rc)
         return list(out[:n.value])
 
+    @staticmethod
+    def last_decode_steps():
+        """Forward steps of this thread's last decode_tokens / decode / decode_batch
+        call (a beam hypothesis may grow by more than one token per step)."""
+        n = C.c_int32(0)
+        check(lib().wh_last_decode_steps(C.byref(n)))
+        return n.value
+
     def decode(self, encoder_out, params: DecoderParams, cancel=None) -> List[Segment]:
         """(*WhisperDecoder).Decode (internal/model/decoder.go:401-410)."""
         return tokens_to_segments(self.decode_tokens(encoder_out, params, cancel), params.prompt)

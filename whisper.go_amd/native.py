@@ -67,6 +67,7 @@ _SIGS = [
     ("wh_f16_to_f32", C.c_float, [C.c_uint16]),
     ("wh_dequantize", C.c_int, [C.c_uint32, _P, C.c_uint64, C.c_uint64, _P, C.c_int32]),
     ("wh_dequantize_noalloc", C.c_int, [C.c_uint32, _P, C.c_uint64, C.c_uint64, _P, C.c_int32]),
+    ("wh_last_decode_steps", C.c_int, [C.POINTER(C.c_int32)]),
     ("wh_matrix_create", C.c_int, [C.c_uint32, C.c_int32, C.c_int32, _P, C.c_uint64, C.c_int32, C.POINTER(_P)]),
     ("wh_matrix_destroy", C.c_int, [_P]),
     ("wh_matrix_bytes", C.c_int, [_P, C.POINTER(C.c_uint64)]),
