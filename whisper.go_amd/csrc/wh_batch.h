@@ -11,12 +11,12 @@
 namespace wh {
 namespace batch {
 
-constexpr int NT = 256;              // threads per workgroup (4 waves, one per SIMD)
+constexpr int NT = 512;              // threads per workgroup (8 waves, two per SIMD)
 constexpr int SMAX = 8;              // streams per launch
 constexpr int XBUDGET = 112 * 1024;  // LDS bytes for staged activation matrices [S][cols]
 constexpr int LNMAX = 2048;          // widest LayerNorm whose weights are staged in LDS
 constexpr int CHUNK = 128;           // keys per cross-attention item
-constexpr int CMAX = 64;             // key chunks per head at most
+constexpr int CMAX = 8;              // key chunks per head at most
 
 struct BLayer {
     MatView sqkv, so, cq, co, fc1, fc2;  // q,k,v stacked [3d, d]
@@ -28,15 +28,16 @@ struct BLayer {
 
 struct BArgs {
     const BLayer *layers;
-    int L, d, H, ctx, V, enc_len, S, chunks;
+    int L, d, H, ctx, V, enc_len, S;
+    int xchunks;                          // key chunks per head in cross attention (S * H * xchunks <= grid)
     size_t kv_stream;                     // floats between two streams' KV caches
     MatView tok;                          // token embedding = tied logits matrix
     const float *pos_emb, *lnw, *lnb;
     const int32_t *tokv, *posv, *active;  // [S]
-    float *x, *x2, *q, *attn, *h, *logits;  // activations [S][d] ([S][4d] for h, [S][V] logits)
+    float *x, *x2, *q, *h, *logits;       // activations [S][d] ([S][4d] for h, [S][V] logits)
     float *sa;                            // self-attention outputs [L][S][d]
-    float *scores, *cmax, *psum, *pv;     // cross-attention scratch [S][H][enc_len] / [S][H][chunks](x64)
-    unsigned *heads;                      // [S][H] chunk counters of the head combine (zero between steps)
+    float *pv, *psum;                     // per chunk of a head: P.V [S][H][xchunks][64], weight sums [S][H][xchunks]
+    uint64_t *xmax;                       // per chunk: {phase, maximum score} pairs [S][H][xchunks]
     unsigned *flags;                      // [grid] barrier phases
     unsigned *err;                        // set when a wait gives up
     float scale;                          // 1/sqrt(64)

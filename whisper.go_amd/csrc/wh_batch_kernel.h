@@ -10,13 +10,16 @@
 // (internal/ml/attention.go:250-256), so its self-attention output
 // sa_l = Wo_l . V0_l + bo_l depends on no activation of the step: all layers'
 // sa_l are computed in the first phase, together with the embedding. A layer is
-// then six phases:
+// then five phases:
 //   B   LN1(x) -> k,v rows into the KV cache at pos (two thirds of the
 //       workgroups); LN2(x + sa_l) -> cross query rows (the other third)
-//   C   cross scores of (state, head, key chunk) items and chunk maxima
-//   D   fast-exp weights against the head maximum, partial P.V per chunk; the
-//       last chunk of a head to finish combines the head -> attn
-//   F   cross out rows: x2 = (x + sa_l) + (Wo_c.attn + b)
+//   X   cross attention: workgroup w takes key chunk c of head h of state s
+//       (the host picks the chunk count so that every item has a workgroup);
+//       scores into LDS, the head maximum from the chunk maxima of the head's
+//       workgroups (a {phase, value} exchange among them, no grid barrier),
+//       fast-exp weights against it and the chunk's partial P.V
+//   F   cross out rows on attn = (sum of the head's partial P.V) / (sum of its
+//       weight sums), combined while staging: x2 = (x + sa_l) + (Wo_c.attn + b)
 //   G   LN3(x2); fc1 rows + GELU -> h
 //   H   fc2 rows: x = x2 + (W2.h + b2)
 // and the step ends with the final LN and the tied logits rows. When a state is
@@ -56,7 +59,7 @@ namespace batch {
 constexpr int NWV = NT / 64;
 constexpr int XBLK = XBUDGET / 128;  // staged 32-float blocks, over all states
 constexpr unsigned SPIN_MAX = 1u << 22;
-constexpr int RW = 4;                // rows per lane group and pass
+constexpr int RW = 2;                // rows per lane group and pass
 
 // ---- cross-lane sums ---------------------------------------------------------------
 __device__ __forceinline__ float wsum(float v) {
@@ -90,6 +93,7 @@ typedef __attribute__((address_space(1))) const uint16_t gcu16;
 typedef __attribute__((address_space(1))) const uint32_t gcu32;
 typedef __attribute__((address_space(1))) const uint64_t gcu64;
 typedef __attribute__((address_space(1))) uint32_t gu32;
+typedef __attribute__((address_space(1))) uint64_t gu64;
 typedef __attribute__((address_space(1))) float gf;
 
 __device__ __forceinline__ float ldg(const float *p) { return *(gcf *)p; }
@@ -211,6 +215,7 @@ struct Lds {
     float *sx;    // their sums
     float *lw, *lb;  // LayerNorm weight and bias
     int *pos;     // [SMAX] positions
+    float *stat;  // [2][SMAX] LayerNorm mean and std
     float *red;   // reduction area (1024 floats)
 };
 
@@ -277,29 +282,21 @@ __device__ __forceinline__ void stage_cols(int S, int cols, int c0, int nbc, Src
 // S states into the staged layout: the mean, then the mean of squared
 // deviations, std = float32(sqrt(float64(var + eps))), w*(x-mean)/std + b. The
 // rows and the weights are loaded in one burst; the statistics take one wave per
-// state, in LDS.
+// state, the normalisation every thread.
 template <class Src>
 __device__ __forceinline__ void stage_ln(int S, int d, Src src, const float *w, const float *bb, const Lds &L, bool sums) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int nbc = d / 32, dq = d / 4;
-    float4 wr[2], br[2];
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const int i = min((int)threadIdx.x + u * NT, dq - 1);
-        wr[u] = ldg4(w + 4 * i);
-        br[u] = ldg4(bb + 4 * i);
-    }
+    const int iw = min((int)threadIdx.x, dq - 1);  // d <= 4 NT
+    const float4 wr = ldg4(w + 4 * iw), br = ldg4(bb + 4 * iw);
     burst(S, d, 0, nbc, src, L.xs);
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const int i = threadIdx.x + u * NT;
-        if (i < dq) {
-            ((float4 *)L.lw)[i] = wr[u];
-            ((float4 *)L.lb)[i] = br[u];
-        }
+    if ((int)threadIdx.x < dq) {
+        ((float4 *)L.lw)[threadIdx.x] = wr;
+        ((float4 *)L.lb)[threadIdx.x] = br;
     }
     __syncthreads();
     float *xf = (float *)L.xs;
+    float *mean_l = L.stat, *sd_l = L.stat + SMAX;
     for (int s = wv; s < S; s += NWV) {
         float t = 0.0f;
 #pragma unroll 8
@@ -312,12 +309,22 @@ __device__ __forceinline__ void stage_ln(int S, int d, Src src, const float *w, 
             q += u * u;
         }
         const float var = wsum(q) / (float)d;
-        const float sd = (float)sqrt((double)(var + 1e-5f));
-#pragma unroll 8
-        for (int i = lane; i < d; i += 64) {
-            float &e = xf[slot(s, nbc, i >> 5, (i & 31) >> 2) * 4 + (i & 3)];
-            e = L.lw[i] * (e - mean) / sd + L.lb[i];
+        if (lane == 0) {
+            mean_l[s] = mean;
+            sd_l[s] = (float)sqrt((double)(var + 1e-5f));
         }
+    }
+    __syncthreads();
+    // four consecutive elements per thread and step
+    for (int i = threadIdx.x; i < S * dq; i += NT) {
+        const int s = i / dq, e = (i - s * dq) * 4;
+        float4 &v = L.xs[slot(s, nbc, e >> 5, (e & 31) >> 2)];
+        const float4 g4 = ((const float4 *)L.lw)[e >> 2], b4 = ((const float4 *)L.lb)[e >> 2];
+        const float m = mean_l[s], sd = sd_l[s];
+        v.x = g4.x * (v.x - m) / sd + b4.x;
+        v.y = g4.y * (v.y - m) / sd + b4.y;
+        v.z = g4.z * (v.z - m) / sd + b4.z;
+        v.w = g4.w * (v.w - m) / sd + b4.w;
     }
     __syncthreads();
     if (sums) {
@@ -327,144 +334,203 @@ __device__ __forceinline__ void stage_ln(int S, int d, Src src, const float *w, 
 }
 
 // ---- GEMV over a row range, all states at once ----------------------------------------
-// Lanes form groups of G: lane l works on row rg + r * (64 / G) + l / G (r < RW,
-// clamped to row1 - 1; the extra rows' results are dropped) and takes staged
-// blocks l % G, l % G + G, ... of [0, nbc) = matrix blocks [c0, c0 + nbc); every
-// decoded chunk of codes feeds the S states.
+// A pass covers NWV * RW * (64 / G) rows from P, interleaved over the waves so
+// that every wave has work when a workgroup has few rows: lanes form groups of G
+// and lane l of wave v works on row P + (r * (64 / G) + l / G) * NWV + v for the
+// wave's first nr slots r (uniform; rows past row1 - 1 are clamped and their
+// results dropped). A lane takes staged blocks l % G, l % G + G, ... of the row.
+template <int G>
+__device__ __forceinline__ int prow(int P, int r) {
+    return P + (r * (64 / G) + (int)(threadIdx.x & 63) / G) * NWV + (int)(threadIdx.x >> 6);
+}
+template <int G>
+__device__ __forceinline__ int pslots(int P, int row1) {
+    constexpr int step = (64 / G) * NWV;
+    const int left = row1 - P - (int)(threadIdx.x >> 6);
+    return left <= 0 ? 0 : min(RW, (left + step - 1) / step);
+}
+
+// Every slot is loaded (rows clamped to row1 - 1), so the compiler's wait counts
+// stay exact across the pipelined units.
 template <int TYPE, int G>
-__device__ __forceinline__ void dots(const MatView &w, int rg, int row1, int S, int c0, int nbc, const float4 *xs,
-                                     const float *sx, float (&acc)[RW][SMAX]) {
-    constexpr int RPS = 64 / G;
-    const int lane = threadIdx.x & 63, ro = lane / G;
-    for (int b = lane % G; b < nbc; b += G) {
-        Blk rb[RW];
+__device__ __forceinline__ void load_blks(const MatView &w, int P, int row1, int c0, int b, Blk (&rb)[RW]) {
 #pragma unroll
-        for (int r = 0; r < RW; r++)
-            blk_load<TYPE>(w, (size_t)min(rg + r * RPS + ro, row1 - 1) * w.nb + c0 + b, rb[r]);
-        float qx[RW][SMAX];
+    for (int r = 0; r < RW; r++) blk_load<TYPE>(w, (size_t)min(prow<G>(P, r), row1 - 1) * w.nb + c0 + b, rb[r]);
+}
+
+// The staged block b of every state against the decoded blocks rb of the lane's
+// rows; every decoded chunk of codes feeds the S states. `valid` false (a lane
+// past the row's last block) leaves acc unchanged.
+template <int TYPE>
+__device__ __forceinline__ void dot_blk(const Blk (&rb)[RW], int nr, int S, int b, int nbc, bool valid,
+                                        const float4 *xs, const float *sx, float (&acc)[RW][SMAX]) {
+    float qx[RW][SMAX];
 #pragma unroll
-        for (int r = 0; r < RW; r++)
+    for (int r = 0; r < RW; r++)
 #pragma unroll
-            for (int s = 0; s < SMAX; s++) qx[r][s] = 0.0f;
+        for (int s = 0; s < SMAX; s++) qx[r][s] = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            // the chunk's codes, made from copies of the raw words that the compiler
-            // cannot see through, so they are not hoisted out for all eight chunks
-            float q[RW][4];
+    for (int k = 0; k < 8; k++) {
+        // the chunk's codes, made from copies of the raw words that the compiler
+        // cannot see through, so they are not hoisted out for all eight chunks
+        float q[RW][4];
 #pragma unroll
-            for (int r = 0; r < RW; r++) {
-                Blk cur = rb[r];
-                asm volatile("" : "+v"(cur.a.x), "+v"(cur.a.y), "+v"(cur.a.z), "+v"(cur.a.w));
-                if constexpr (TYPE == 8) asm volatile("" : "+v"(cur.b.x), "+v"(cur.b.y), "+v"(cur.b.z), "+v"(cur.b.w));
-                if constexpr (TYPE == 6 || TYPE == 7) asm volatile("" : "+v"(cur.h));
-                codes4<TYPE>(cur, k, q[r]);
-            }
-#pragma unroll
-            for (int s = 0; s < SMAX; s++)
-                if (s < S) {
-                    const float4 xv = xs[slot(s, nbc, b, k)];
-#pragma unroll
-                    for (int r = 0; r < RW; r++) {
-                        float &c = qx[r][s];
-                        c = __builtin_fmaf(q[r][0], xv.x, c);
-                        c = __builtin_fmaf(q[r][1], xv.y, c);
-                        c = __builtin_fmaf(q[r][2], xv.z, c);
-                        c = __builtin_fmaf(q[r][3], xv.w, c);
-                    }
-                }
-            // keep the next chunk's LDS reads after these FMAs
-            asm volatile("" ::: "memory");
+        for (int r = 0; r < RW; r++) {
+            if (r >= nr) continue;
+            Blk cur = rb[r];
+            asm volatile("" : "+v"(cur.a.x), "+v"(cur.a.y), "+v"(cur.a.z), "+v"(cur.a.w));
+            if constexpr (TYPE == 8) asm volatile("" : "+v"(cur.b.x), "+v"(cur.b.y), "+v"(cur.b.z), "+v"(cur.b.w));
+            if constexpr (TYPE == 6 || TYPE == 7) asm volatile("" : "+v"(cur.h));
+            codes4<TYPE>(cur, k, q[r]);
         }
 #pragma unroll
         for (int s = 0; s < SMAX; s++)
             if (s < S) {
-                const float bsum = TYPE == 8 ? 0.0f : sx[s * nbc + b];
+                const float4 xv = xs[slot(s, nbc, b, k)];
 #pragma unroll
-                for (int r = 0; r < RW; r++) acc[r][s] += bscale<TYPE>(rb[r], qx[r][s], bsum);
+                for (int r = 0; r < RW; r++) {
+                    if (r >= nr) continue;
+                    float &c = qx[r][s];
+                    c = __builtin_fmaf(q[r][0], xv.x, c);
+                    c = __builtin_fmaf(q[r][1], xv.y, c);
+                    c = __builtin_fmaf(q[r][2], xv.z, c);
+                    c = __builtin_fmaf(q[r][3], xv.w, c);
+                }
             }
+        // keep the next chunk's LDS reads after these FMAs
+        asm volatile("" ::: "memory");
     }
+#pragma unroll
+    for (int s = 0; s < SMAX; s++)
+        if (s < S) {
+            const float bsum = TYPE == 8 ? 0.0f : sx[s * nbc + b];
+#pragma unroll
+            for (int r = 0; r < RW; r++)
+                if (r < nr) {
+                    const float v = bscale<TYPE>(rb[r], qx[r][s], bsum);
+                    acc[r][s] += valid ? v : 0.0f;
+                }
+        }
 }
 
-// The epilogue operands pre(s, row) of the lane's rows, loaded before the dot
-// products so that their latency overlaps the weight loads.
+// The epilogue operand pre(s, row) of each of the lane's rows for the state the
+// lane finishes (lane % G), loaded before the dot products so that its latency
+// overlaps the weight loads.
 template <int G, class Pre>
-__device__ __forceinline__ void load_pre(int rg, int row1, int S, Pre pre, float2 (&ad)[RW][SMAX]) {
-    constexpr int RPS = 64 / G;
-    const int ro = (threadIdx.x & 63) / G;
+__device__ __forceinline__ void load_pre(int P, int row1, int S, Pre pre, float2 (&ad)[RW]) {
+    const int st = min((int)(threadIdx.x & 63) % G, S - 1);
+#pragma unroll
+    for (int r = 0; r < RW; r++) ad[r] = pre(st, min(prow<G>(P, r), row1 - 1));
+}
+
+// Row sums over the lane groups; lane s of a group runs the epilogue of state s.
+template <int G, class Epi>
+__device__ __forceinline__ void finish(int P, int nr, int row1, int S, unsigned amask, float (&acc)[RW][SMAX],
+                                       const float2 (&ad)[RW], Epi epi) {
+    const int gl = (int)(threadIdx.x & 63) % G;
 #pragma unroll
     for (int r = 0; r < RW; r++) {
-        const int row = min(rg + r * RPS + ro, row1 - 1);
-#pragma unroll
-        for (int s = 0; s < SMAX; s++) ad[r][s] = s < S ? pre(s, row) : make_float2(0.f, 0.f);
-    }
-}
-
-template <int G, class Epi>
-__device__ __forceinline__ void finish(int rg, int row1, int S, unsigned amask, float (&acc)[RW][SMAX],
-                                       const float2 (&ad)[RW][SMAX], Epi epi) {
-    constexpr int RPS = 64 / G;
-    const int lane = threadIdx.x & 63, ro = lane / G;
-#pragma unroll
-    for (int r = 0; r < RW; r++)
+        if (r >= nr) continue;
+        const int row = prow<G>(P, r);
+        float mine = 0.0f;
 #pragma unroll
         for (int s = 0; s < SMAX; s++)
             if (s < S) {
                 const float v = gsum<G>(acc[r][s]);
-                const int row = rg + r * RPS + ro;
-                if (lane % G == 0 && row < row1 && ((amask >> s) & 1u)) epi(s, row, v, ad[r][s]);
+                mine = gl == s ? v : mine;
             }
+        if (gl < S && row < row1 && ((amask >> gl) & 1u)) epi(gl, row, mine, ad[r]);
+    }
 }
 
-// Rows [row0, row1) of w against the staged input (already in LDS when `staged`,
-// else staged here from src in passes of as many blocks as fit). A workgroup
-// without rows returns at once (uniformly).
-template <int TYPE, int G, class Src, class Pre, class Epi>
-__device__ __forceinline__ void gemv(const MatView &w, int row0, int row1, int S, unsigned amask, bool staged, Src src,
+// Rows [row0, row1) of w against inputs that stage() puts in LDS (all columns).
+// A workgroup without rows returns at once (uniformly). The work is a sequence
+// of units (row pass, block step); the first two units' weight blocks and the
+// first pass's epilogue operands are loaded before stage() runs, and every unit
+// loads the blocks of the unit two ahead while it computes.
+template <int TYPE, int G, class Stage, class Pre, class Epi>
+__device__ __forceinline__ void gemv(const MatView &w, int row0, int row1, int S, unsigned amask, Stage stage,
                                      const Lds &L, Pre pre, Epi epi) {
-    gemv_g<TYPE, G>(w, row0, row1, S, amask, staged, src, L, pre, epi);
-}
-
-template <int TYPE, int G, class Src, class Pre, class Epi>
-__device__ __forceinline__ void gemv_g(const MatView &w, int row0, int row1, int S, unsigned amask, bool staged, Src src,
-                       const Lds &L, Pre pre, Epi epi) {
     if (row0 >= row1) return;
-    constexpr int WR = RW * (64 / G);  // rows of a wave's pass
-    const int wv = threadIdx.x >> 6, nb = w.nb, per = XBLK / S;
-    if (staged || nb <= per) {
-        if (!staged) stage_cols(S, w.cols, 0, nb, src, L.xs, L.sx, TYPE != 8);
-        for (int rg = row0 + wv * WR; rg < row1; rg += NWV * WR) {
-            float2 ad[RW][SMAX];
-            load_pre<G>(rg, row1, S, pre, ad);
-            float acc[RW][SMAX];
+    constexpr int PR = NWV * RW * (64 / G);  // rows of a workgroup's pass
+    const int nb = w.nb, gl = (int)(threadIdx.x & 63) % G;
+    const int NBJ = (nb + G - 1) / G, NU = (row1 - row0 + PR - 1) / PR * NBJ;
+    const auto unit = [&](int u, Blk (&rb)[RW]) __attribute__((always_inline)) {
+        const int p = u / NBJ, j = u - p * NBJ;
+        load_blks<TYPE, G>(w, row0 + p * PR, row1, 0, min(gl + j * G, nb - 1), rb);
+    };
+    Blk b0[RW], b1[RW], b2[RW];
+    float acc[RW][SMAX];
+    float2 ad[RW];
+    unit(0, b0);
+    unit(min(1, NU - 1), b1);
+    load_pre<G>(row0, row1, S, pre, ad);
+    stage();
+    for (int u = 0; u < NU; u++) {
+        const int p = u / NBJ, j = u - p * NBJ, P = row0 + p * PR, nr = pslots<G>(P, row1);
+        if (j == 0) {
 #pragma unroll
             for (int r = 0; r < RW; r++)
 #pragma unroll
                 for (int s = 0; s < SMAX; s++) acc[r][s] = 0.0f;
-            dots<TYPE, G>(w, rg, row1, S, 0, nb, L.xs, L.sx, acc);
-            finish<G>(rg, row1, S, amask, acc, ad, epi);
+            if (u > 0) load_pre<G>(P, row1, S, pre, ad);
         }
-    } else {
-        // passes over the columns; each wave keeps its rows' sums across the passes
-        // (the host sizes the grid so a workgroup has at most NWV * WR rows here)
-        const int rg = row0 + wv * WR;
-        float2 ad[RW][SMAX];
-        load_pre<G>(rg, row1, S, pre, ad);
-        float acc[RW][SMAX];
+        unit(min(u + 2, NU - 1), b2);
+        const int b = gl + j * G;
+        dot_blk<TYPE>(b0, nr, S, min(b, nb - 1), nb, b < nb, L.xs, L.sx, acc);
+        if (j == NBJ - 1) finish<G>(P, nr, row1, S, amask, acc, ad, epi);
 #pragma unroll
-        for (int r = 0; r < RW; r++)
-#pragma unroll
-            for (int s = 0; s < SMAX; s++) acc[r][s] = 0.0f;
-        for (int c0 = 0; c0 < nb; c0 += per) {
-            const int nbc = min(per, nb - c0);
-            stage_cols(S, w.cols, c0, nbc, src, L.xs, L.sx, TYPE != 8);
-            if (rg < row1) dots<TYPE, G>(w, rg, row1, S, c0, nbc, L.xs, L.sx, acc);
-            __syncthreads();
+        for (int r = 0; r < RW; r++) {
+            b0[r] = b1[r];
+            b1[r] = b2[r];
         }
-        if (rg < row1) finish<G>(rg, row1, S, amask, acc, ad, epi);
     }
     __syncthreads();
 }
 
+// Rows [row0, row1) of w when the S states' input rows do not fit in LDS: passes
+// over the columns, staged from src; each wave keeps its rows' sums across the
+// passes (the host sizes the grid so a workgroup has at most one pass of rows).
+template <int TYPE, int G, class Src, class Pre, class Epi>
+__device__ __forceinline__ void gemv_cols(const MatView &w, int row0, int row1, int S, unsigned amask, Src src,
+                                          const Lds &L, Pre pre, Epi epi) {
+    if (row0 >= row1) return;
+    const int nb = w.nb, per = XBLK / S, gl = (int)(threadIdx.x & 63) % G;
+    const int nr = pslots<G>(row0, row1);
+    float2 ad[RW];
+    load_pre<G>(row0, row1, S, pre, ad);
+    float acc[RW][SMAX];
+#pragma unroll
+    for (int r = 0; r < RW; r++)
+#pragma unroll
+        for (int s = 0; s < SMAX; s++) acc[r][s] = 0.0f;
+    for (int c0 = 0; c0 < nb; c0 += per) {
+        const int nbc = min(per, nb - c0);
+        stage_cols(S, w.cols, c0, nbc, src, L.xs, L.sx, TYPE != 8);
+        if (nr > 0)
+            for (int b = gl; b < nbc; b += G) {
+                Blk rb[RW];
+                load_blks<TYPE, G>(w, row0, row1, c0, b, rb);
+                dot_blk<TYPE>(rb, nr, S, b, nbc, true, L.xs, L.sx, acc);
+            }
+        __syncthreads();
+    }
+    if (nr > 0) finish<G>(row0, nr, row1, S, amask, acc, ad, epi);
+    __syncthreads();
+}
+
+// All columns staged from src when they fit, else column passes.
+template <int TYPE, int G, class Src, class Pre, class Epi>
+__device__ __forceinline__ void gemv_src(const MatView &w, int row0, int row1, int S, unsigned amask, Src src,
+                                         const Lds &L, Pre pre, Epi epi) {
+    if (w.nb <= XBLK / S)
+        gemv<TYPE, G>(
+            w, row0, row1, S, amask,
+            [&]() __attribute__((always_inline)) { stage_cols(S, w.cols, 0, w.nb, src, L.xs, L.sx, TYPE != 8); }, L,
+            pre, epi);
+    else
+        gemv_cols<TYPE, G>(w, row0, row1, S, amask, src, L, pre, epi);
+}
 
 __device__ __forceinline__ int split(int n, int w, int W) { return (int)((long)n * w / W); }
 
@@ -479,10 +545,11 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
     L.lw = L.sx + XBLK;
     L.lb = L.lw + LNMAX;
     L.pos = (int *)(L.lb + LNMAX);
+    L.stat = (float *)(L.pos + 16);
     L.red = (float *)(L.pos + 64);
     BLayer *lyl = (BLayer *)(L.red + 1024);  // the layer descriptors, copied once
     const int W = (int)gridDim.x, w = (int)blockIdx.x;
-    const int S = a.S, d = a.d, H = a.H, Ln = a.L, C = a.chunks;
+    const int S = a.S, d = a.d, H = a.H, Ln = a.L;
     {
         const int n = Ln * (int)(sizeof(BLayer) / 8);
         for (int i = threadIdx.x; i < n; i += NT) ((uint64_t *)lyl)[i] = ((gcu64 *)a.layers)[i];
@@ -504,29 +571,28 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
 
     const int ctx = a.ctx, enc_len = a.enc_len;
     const size_t kvs = a.kv_stream, plane = (size_t)H * ctx * 64;
-    float *xg = a.x, *x2g = a.x2, *qg = a.q, *attng = a.attn, *hg = a.h, *sag = a.sa;
+    float *xg = a.x, *x2g = a.x2, *qg = a.q, *hg = a.h, *sag = a.sa;
     const int *posl = L.pos;
-    const auto nosrc = [](int, int) { return make_float4(0.f, 0.f, 0.f, 0.f); };
     const auto nopre = [](int, int) { return make_float2(0.f, 0.f); };
     // rows of this layer's self-attention output sa_l = Wo V0 + bo (V0: KV row 0)
     const auto sa_rows = [&](const BLayer *ly, float *sal, int r0, int r1) __attribute__((always_inline)) {
         const float *vp = ly->kv + plane;
         const float *sob = ly->sob;
-        gemv<TYPE, G>(
-            ly->so, r0, r1, S, amask, false,
+        gemv_src<TYPE, G>(
+            ly->so, r0, r1, S, amask,
             [=](int s, int c) { return ldx4(vp + (size_t)s * kvs + (size_t)(c >> 6) * ctx * 64 + (c & 63)); }, L,
             [=](int, int r) { return make_float2(0.f, ldg(sob + r)); },
             [=](int s, int r, float v, float2 p) { stx(sal + (size_t)s * d + r, v + p.y); });
     };
     // k,v rows [d + r0, d + r1) of the stacked q,k,v matrix into the KV cache at pos
     const auto kv_rows = [&](const BLayer *ly, int r0, int r1) __attribute__((always_inline)) {
-        if (r0 >= r1) return;
-        const float *xr = xg;
-        stage_ln(S, d, [=](int s, int c) { return ldx4(xr + (size_t)s * d + c); }, ly->ln1w, ly->ln1b, L,
-                 TYPE != 8);
+        const float *xr = xg, *lw = ly->ln1w, *lb = ly->ln1b;
         float *kv = ly->kv;
         const float *svb = ly->svb;
-        gemv<TYPE, G>(ly->sqkv, d + r0, d + r1, S, amask, true, nosrc, L,
+        gemv<TYPE, G>(ly->sqkv, d + r0, d + r1, S, amask,
+                   [&]() __attribute__((always_inline)) {
+                       stage_ln(S, d, [=](int s, int c) { return ldx4(xr + (size_t)s * d + c); }, lw, lb, L, TYPE != 8);
+                   }, L,
                    [=](int, int r) { return make_float2(0.f, r >= 2 * d ? ldg(svb + r - 2 * d) : 0.0f); },
                    [=](int s, int r, float v, float2 p) {
                        const int j = r % d;
@@ -537,18 +603,19 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
     };
     // cross query rows [r0, r1) from LN2(x + sa_l)
     const auto cq_rows = [&](const BLayer *ly, const float *sal, int r0, int r1) __attribute__((always_inline)) {
-        if (r0 >= r1) return;
-        const float *xr = xg;
-        stage_ln(
-            S, d,
-            [=](int s, int c) {
-                const float4 u = ldx4(xr + (size_t)s * d + c), v = ldx4(sal + (size_t)s * d + c);
-                return make_float4(u.x + v.x, u.y + v.y, u.z + v.z, u.w + v.w);
-            },
-            ly->ln2w, ly->ln2b, L, TYPE != 8);
+        const float *xr = xg, *lw = ly->ln2w, *lb = ly->ln2b;
         const float *cqb = ly->cqb;
         float *qw = qg;
-        gemv<TYPE, G>(ly->cq, r0, r1, S, amask, true, nosrc, L, [=](int, int r) { return make_float2(0.f, ldg(cqb + r)); },
+        gemv<TYPE, G>(ly->cq, r0, r1, S, amask,
+                   [&]() __attribute__((always_inline)) {
+                       stage_ln(
+                           S, d,
+                           [=](int s, int c) {
+                               const float4 u = ldx4(xr + (size_t)s * d + c), v = ldx4(sal + (size_t)s * d + c);
+                               return make_float4(u.x + v.x, u.y + v.y, u.z + v.z, u.w + v.w);
+                           },
+                           lw, lb, L, TYPE != 8);
+                   }, L, [=](int, int r) { return make_float2(0.f, ldg(cqb + r)); },
                    [=](int s, int r, float v, float2 p) { stx(qw + (size_t)s * d + r, v + p.y); });
     };
 
@@ -585,127 +652,161 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
             cq_rows(ly, sal, split(d, w - Wk, W - Wk), split(d, w + 1 - Wk, W - Wk));
         }
         gbar(flags, errw, g);
-        // ---- C: scores of (state, head, chunk) items and chunk maxima ----
-        for (int it = w; it < S * H * C; it += W) {
-            const int s = it / (H * C), h = (it / C) % H, c = it % C;
-            if (!((amask >> s) & 1u)) continue;
-            const int q16 = lane & 15;
-            const float4 q4 = ldx4(qg + (size_t)s * d + h * 64 + q16 * 4);
-            const float *K = (const float *)((gcu64 *)ly->kbase)[s] + (size_t)h * enc_len * 64;
-            const int t0 = c * CHUNK, t1 = min(t0 + CHUNK, enc_len);
-            float4 k4[CHUNK / 16];
-#pragma unroll
-            for (int j = 0; j < CHUNK / 16; j++) {
-                const int t = t0 + j * 16 + wv * 4 + (lane >> 4);
-                k4[j] = t < t1 ? ldg4(K + (size_t)t * 64 + q16 * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int j = 0; j < CHUNK / 16; j++) {
-                const int t = t0 + j * 16 + wv * 4 + (lane >> 4);
-                float dot = q4.x * k4[j].x + q4.y * k4[j].y + q4.z * k4[j].z + q4.w * k4[j].w;
-#pragma unroll
-                for (int o = 8; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 64);
-                if (t < t1) {
-                    const float sco = dot * a.scale;
-                    if (q16 == 0) stx(a.scores + ((size_t)s * H + h) * enc_len + t, sco);
-                    mx = fmaxf(mx, sco);
-                }
-            }
-            mx = wmax(mx);
-            if (lane == 0) L.red[wv] = mx;
-            __syncthreads();
-            if (threadIdx.x == 0) {
-                float m = L.red[0];
-                for (int i = 1; i < NWV; i++) m = fmaxf(m, L.red[i]);
-                stx(a.cmax + it, m);
-            }
-            __syncthreads();
-        }
-        gbar(flags, errw, g);
-        // ---- D: fast-exp weights against the head maximum, partial P.V; head combine ----
-        for (int it = w; it < S * H * C; it += W) {
-            const int s = it / (H * C), h = (it / C) % H, c = it % C;
-            if (!((amask >> s) & 1u)) continue;
-            const int q16 = lane & 15;
-            const size_t sh = (size_t)s * H + h;
-            float M = lane < C ? ldx(a.cmax + sh * C + lane) : -INFINITY;
-            const float *V = (const float *)((gcu64 *)ly->vbase)[s] + (size_t)h * enc_len * 64;
-            const float *sc = a.scores + sh * enc_len;
-            const int t0 = c * CHUNK, t1 = min(t0 + CHUNK, enc_len);
-            float sv[CHUNK / 16];
-            float4 v4[CHUNK / 16];
-#pragma unroll
-            for (int j = 0; j < CHUNK / 16; j++) {
-                const int t = t0 + j * 16 + wv * 4 + (lane >> 4);
-                sv[j] = t < t1 ? ldx(sc + t) : 0.0f;
-                v4[j] = t < t1 ? ldg4(V + (size_t)t * 64 + q16 * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-            M = wmax(M);
-            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-            float es = 0.0f;
-#pragma unroll
-            for (int j = 0; j < CHUNK / 16; j++) {
-                const int t = t0 + j * 16 + wv * 4 + (lane >> 4);
-                if (t < t1) {
-                    const float e = fast_exp(sv[j] - M);
-                    acc.x += e * v4[j].x; acc.y += e * v4[j].y; acc.z += e * v4[j].z; acc.w += e * v4[j].w;
-                    if (q16 == 0) es += e;
-                }
-            }
-#pragma unroll
-            for (int o = 16; o < 64; o <<= 1) {
-                acc.x += __shfl_xor(acc.x, o, 64);
-                acc.y += __shfl_xor(acc.y, o, 64);
-                acc.z += __shfl_xor(acc.z, o, 64);
-                acc.w += __shfl_xor(acc.w, o, 64);
-            }
-            es = wsum(es);
-            float4 *red4 = (float4 *)L.red;  // [NWV][16]
-            if (lane < 16) red4[wv * 16 + lane] = acc;
-            if (lane == 0) L.red[512 + wv] = es;
-            __syncthreads();
-            if (threadIdx.x < 16) {
-                float4 r = red4[threadIdx.x];
-                for (int i = 1; i < NWV; i++) {
-                    const float4 t4 = red4[i * 16 + threadIdx.x];
-                    r.x += t4.x; r.y += t4.y; r.z += t4.z; r.w += t4.w;
-                }
-                float *dst = a.pv + (size_t)it * 64 + threadIdx.x * 4;
-                stx(dst, r.x); stx(dst + 1, r.y); stx(dst + 2, r.z); stx(dst + 3, r.w);
-            }
-            if (threadIdx.x == 0) {
-                float t = 0.0f;
-                for (int i = 0; i < NWV; i++) t += L.red[512 + i];
-                stx(a.psum + it, t);
-            }
-            // the last chunk of the head to get here combines the head's chunks
-            stores_done();
-            __syncthreads();
-            int *last = (int *)(L.red + 520);
-            if (threadIdx.x == 0)
-                *last = __hip_atomic_fetch_add(a.heads + sh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                        (unsigned)(C - 1);
-            __syncthreads();
-            if (*last && threadIdx.x < 64) {
-                const float ps = lane < C ? ldx(a.psum + sh * C + lane) : 0.0f;
-                float o = 0.0f;
-#pragma unroll 4
-                for (int i = 0; i < C; i++) o += ldx(a.pv + (sh * C + i) * 64 + lane);
-                const float sum = wsum(ps);
-                stx(attng + (size_t)s * d + h * 64 + lane, o * (1.0f / sum));
-                if (lane == 0) __hip_atomic_store(a.heads + sh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            __syncthreads();
-        }
-        gbar(flags, errw, g);
-        // ---- F: cross out rows; x2 = (x + sa_l) + (Wo_c.attn + b) ----
+        // ---- X: cross attention; item (state, head, key chunk) on workgroup w ----
         {
-            const float *cob = ly->cob, *xr = xg, *ar = attng;
+            const int XC = a.xchunks, it = w, klen = (enc_len + XC - 1) / XC;
+            const int s = it / (H * XC), h = (it / XC) % H, c = it % XC;
+            if (it < S * H * XC && ((amask >> s) & 1u)) {
+                constexpr int KG = 4 * NWV;  // keys per step: 16 lanes per key
+                constexpr int XS = 12;       // steps per batch
+                const int q16 = lane & 15, kq = wv * 4 + (lane >> 4);  // the lane's key of a step
+                const size_t sh = (size_t)s * H + h;
+                const float4 q4 = ldx4(qg + (size_t)s * d + h * 64 + q16 * 4);
+                const float *K = (const float *)((gcu64 *)ly->kbase)[s] + (size_t)h * enc_len * 64;
+                const float *V = (const float *)((gcu64 *)ly->vbase)[s] + (size_t)h * enc_len * 64;
+                const int t0 = c * klen, t1 = min(t0 + klen, enc_len);
+                float *scl = (float *)L.xs;  // the chunk's scores
+                // scores, XS steps per batch, the next batch's K loads in flight
+                float mx = -INFINITY;
+                float4 kb[XS];
+#pragma unroll
+                for (int j = 0; j < XS; j++) {
+                    const int t = t0 + j * KG + kq;
+                    kb[j] = t < t1 ? ldg4(K + (size_t)t * 64 + q16 * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+                for (int tb = t0; tb < t1; tb += XS * KG) {
+                    float4 kn[XS];
+#pragma unroll
+                    for (int j = 0; j < XS; j++) {
+                        const int t = tb + XS * KG + j * KG + kq;
+                        kn[j] = t < t1 ? ldg4(K + (size_t)t * 64 + q16 * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                    }
+#pragma unroll
+                    for (int j = 0; j < XS; j++) {
+                        const int t = tb + j * KG + kq;
+                        float dot = q4.x * kb[j].x + q4.y * kb[j].y + q4.z * kb[j].z + q4.w * kb[j].w;
+#pragma unroll
+                        for (int o = 8; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 64);
+                        if (t < t1) {
+                            const float sco = dot * a.scale;
+                            if (q16 == 0) scl[t - t0] = sco;
+                            mx = fmaxf(mx, sco);
+                        }
+                    }
+#pragma unroll
+                    for (int j = 0; j < XS; j++) kb[j] = kn[j];
+                }
+                // the first V batch loads, independent of the maximum, go out now
+                float4 vb[XS];
+#pragma unroll
+                for (int j = 0; j < XS; j++) {
+                    const int t = t0 + j * KG + kq;
+                    vb[j] = t < t1 ? ldg4(V + (size_t)t * 64 + q16 * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+                mx = wmax(mx);
+                if (lane == 0) L.red[wv] = mx;
+                __syncthreads();
+                float M = L.red[0];
+                for (int i = 1; i < NWV; i++) M = fmaxf(M, L.red[i]);
+                // the head maximum: the chunk maxima of the head's workgroups, exchanged as
+                // {phase, value} pairs (no grid barrier)
+                if (XC > 1) {
+                    if (threadIdx.x == 0)
+                        __hip_atomic_store((gu64 *)(a.xmax + it), ((uint64_t)g << 32) | __float_as_uint(M),
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (threadIdx.x < 64) {
+                        gcu64 *src = (gcu64 *)(a.xmax + sh * XC);
+                        const int li = min(lane, XC - 1);
+                        uint64_t v = __hip_atomic_load(src + li, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        for (unsigned spins = 0;; spins++) {
+                            if (__all((unsigned)(v >> 32) >= g)) break;
+                            if (__any(failed(errw) || spins > SPIN_MAX)) {
+                                if (lane == 0) atomicOr(errw, 1u);
+                                break;
+                            }
+                            if ((unsigned)(v >> 32) < g)
+                                v = __hip_atomic_load(src + li, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        }
+                        const float m = wmax(__uint_as_float((uint32_t)v));
+                        if (lane == 0) L.red[8] = m;
+                    }
+                    __syncthreads();
+                    M = L.red[8];
+                }
+                // fast-exp weights against the head maximum and the chunk's P.V
+                float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+                float es = 0.0f;
+                for (int tb = t0; tb < t1; tb += XS * KG) {
+                    float4 vn[XS];
+#pragma unroll
+                    for (int j = 0; j < XS; j++) {
+                        const int t = tb + XS * KG + j * KG + kq;
+                        vn[j] = t < t1 ? ldg4(V + (size_t)t * 64 + q16 * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                    }
+#pragma unroll
+                    for (int j = 0; j < XS; j++) {
+                        const int t = tb + j * KG + kq;
+                        if (t < t1) {
+                            const float e = fast_exp(scl[t - t0] - M);
+                            acc.x += e * vb[j].x; acc.y += e * vb[j].y; acc.z += e * vb[j].z; acc.w += e * vb[j].w;
+                            if (q16 == 0) es += e;
+                        }
+                    }
+#pragma unroll
+                    for (int j = 0; j < XS; j++) vb[j] = vn[j];
+                }
+#pragma unroll
+                for (int o = 16; o < 64; o <<= 1) {
+                    acc.x += __shfl_xor(acc.x, o, 64);
+                    acc.y += __shfl_xor(acc.y, o, 64);
+                    acc.z += __shfl_xor(acc.z, o, 64);
+                    acc.w += __shfl_xor(acc.w, o, 64);
+                }
+                es = wsum(es);
+                float4 *red4 = (float4 *)(L.red + 64);  // [NWV][16]
+                if (lane < 16) red4[wv * 16 + lane] = acc;
+                if (lane == 0) L.red[16 + wv] = es;
+                __syncthreads();
+                if (threadIdx.x < 16) {
+                    float4 r = red4[threadIdx.x];
+                    for (int i = 1; i < NWV; i++) {
+                        const float4 t4 = red4[i * 16 + threadIdx.x];
+                        r.x += t4.x; r.y += t4.y; r.z += t4.z; r.w += t4.w;
+                    }
+                    float *dst = a.pv + (size_t)it * 64 + threadIdx.x * 4;
+                    stx(dst, r.x); stx(dst + 1, r.y); stx(dst + 2, r.z); stx(dst + 3, r.w);
+                }
+                if (threadIdx.x == 0) {
+                    float t = 0.0f;
+                    for (int i = 0; i < NWV; i++) t += L.red[16 + i];
+                    stx(a.psum + it, t);
+                }
+            }
+        }
+        gbar(flags, errw, g);
+        // ---- F: cross out rows on the combined heads; x2 = (x + sa_l) + (Wo_c.attn + b) ----
+        {
+            const float *cob = ly->cob, *xr = xg, *pvr = a.pv, *psr = a.psum;
             float *x2w = x2g;
-            gemv<TYPE, G>(
-                ly->co, split(d, w, W), split(d, w + 1, W), S, amask, false,
-                [=](int s, int c) { return ldx4(ar + (size_t)s * d + c); }, L,
+            const int XC = a.xchunks;
+            gemv_src<TYPE, G>(
+                ly->co, split(d, w, W), split(d, w + 1, W), S, amask,
+                [=](int s, int c) {
+                    // head h of state s: its chunks' P.V over their weight sums
+                    const size_t b = ((size_t)s * H + (c >> 6)) * XC;
+                    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < CMAX; i++) {
+                        if (i >= XC) break;
+                        const float4 p4 = ldx4(pvr + (b + i) * 64 + (c & 63));
+                        o.x += p4.x; o.y += p4.y; o.z += p4.z; o.w += p4.w;
+                        sum += ldx(psr + b + i);
+                    }
+                    const float inv = 1.0f / sum;
+                    return make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+                },
+                L,
                 [=](int s, int r) {
                     return make_float2(ldx(xr + (size_t)s * d + r) + ldx(sal + (size_t)s * d + r), ldg(cob + r));
                 },
@@ -716,11 +817,13 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
         {
             const int r0 = split(4 * d, w, W), r1 = split(4 * d, w + 1, W);
             if (r0 < r1) {
-                const float *x2r = x2g, *fc1b = ly->fc1b;
+                const float *x2r = x2g, *fc1b = ly->fc1b, *lw = ly->ln3w, *lb = ly->ln3b;
                 float *hw = hg;
-                stage_ln(S, d, [=](int s, int c) { return ldx4(x2r + (size_t)s * d + c); }, ly->ln3w, ly->ln3b, L,
-                         TYPE != 8);
-                gemv<TYPE, G>(ly->fc1, r0, r1, S, amask, true, nosrc, L,
+                gemv<TYPE, G>(ly->fc1, r0, r1, S, amask,
+                           [&]() __attribute__((always_inline)) {
+                               stage_ln(S, d, [=](int s, int c) { return ldx4(x2r + (size_t)s * d + c); }, lw, lb, L,
+                                        TYPE != 8);
+                           }, L,
                            [=](int, int r) { return make_float2(0.f, ldg(fc1b + r)); },
                            [=](int s, int r, float v, float2 p) { stx(hw + (size_t)s * 4 * d + r, gelu_ref(v + p.y)); });
             }
@@ -730,8 +833,8 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
         {
             const float *fc2b = ly->fc2b, *hr = hg, *x2r = x2g;
             float *xw = xg;
-            gemv<TYPE, G>(
-                ly->fc2, split(d, w, W), split(d, w + 1, W), S, amask, false,
+            gemv_src<TYPE, G>(
+                ly->fc2, split(d, w, W), split(d, w + 1, W), S, amask,
                 [=](int s, int c) { return ldx4(hr + (size_t)s * 4 * d + c); }, L,
                 [=](int s, int r) { return make_float2(ldx(x2r + (size_t)s * d + r), ldg(fc2b + r)); },
                 [=](int s, int r, float v, float2 p) { stx(xw + (size_t)s * d + r, p.x + (v + p.y)); });
@@ -742,11 +845,14 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
     {
         const int r0 = split(a.V, w, W), r1 = split(a.V, w + 1, W);
         if (r0 < r1) {
-            const float *xr = xg;
+            const float *xr = xg, *lw = a.lnw, *lb = a.lnb;
             float *lg = a.logits;
             const int V = a.V;
-            stage_ln(S, d, [=](int s, int c) { return ldx4(xr + (size_t)s * d + c); }, a.lnw, a.lnb, L, TYPE != 8);
-            gemv<TYPE, G>(a.tok, r0, r1, S, amask, true, nosrc, L, nopre,
+            gemv<TYPE, G>(a.tok, r0, r1, S, amask,
+                       [&]() __attribute__((always_inline)) {
+                           stage_ln(S, d, [=](int s, int c) { return ldx4(xr + (size_t)s * d + c); }, lw, lb, L,
+                                    TYPE != 8);
+                       }, L, nopre,
                        [=](int s, int r, float v, float2) { stg(lg + (size_t)s * V + r, v); });
         }
     }

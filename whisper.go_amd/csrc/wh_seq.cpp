@@ -455,8 +455,12 @@ int batch_setup(wh_seq &s) {
     const int W = std::min(env_int("WHISPER_HIP_GRID", cus), cus);
     // LDS for the staged [S][d] inputs and the LayerNorm weights; the fc2 column
     // passes keep <= 16 rows per workgroup; a head has at most CMAX key chunks
+    // cross attention: every (state, head, key chunk) item has a workgroup; a chunk's
+    // scores stay in LDS
+    const int xchunks = std::min(std::max(1, W / (s.S * H)), batch::CMAX);
     if (W < 8 || (size_t)lds_max < batch::LDS_BYTES || (d + W - 1) / W > 16 || d > batch::LNMAX || L > batch::LMAX ||
-        s.S * (d / 32) > batch::XBUDGET / 128 || s.cb.chunks > batch::CMAX)
+        s.S * (d / 32) > batch::XBUDGET / 128 || s.S * H > W ||
+        (size_t)(s.enc_len + xchunks - 1) / xchunks * sizeof(float) > (size_t)batch::XBUDGET)
         return WH_OK;
     std::vector<batch::BLayer> ly(L);
     for (int li = 0; li < L; li++) {
@@ -477,18 +481,18 @@ int batch_setup(wh_seq &s) {
     batch::BArgs &a = s.bargs;
     a.layers = dl;
     a.L = L; a.d = d; a.H = H; a.ctx = m.n_ctx; a.V = m.n_vocab; a.enc_len = s.enc_len; a.S = s.S;
-    a.chunks = s.cb.chunks;
+    a.xchunks = xchunks;
     a.kv_stream = s.kv_stream;
     a.tok = view(m.tok);
     a.pos_emb = m.pos; a.lnw = m.lnw; a.lnb = m.lnb;
     a.tokv = s.tok; a.posv = s.pos; a.active = s.active;
-    a.x = s.x; a.q = s.q; a.attn = s.attn; a.h = s.h; a.logits = s.logits;
-    if ((rc = s.alloc(&a.x2, (size_t)s.S * d)) || (rc = s.alloc(&a.sa, (size_t)L * s.S * d))) return rc;
-    a.scores = s.cb.scores; a.cmax = s.cb.cmax; a.psum = s.cb.psum; a.pv = s.cb.pv;
-    if ((rc = s.alloc(&a.heads, (size_t)s.S * H)) || (rc = s.alloc(&a.flags, (size_t)W)) ||
-        (rc = s.alloc(&a.err, 1)))
+    a.x = s.x; a.q = s.q; a.h = s.h; a.logits = s.logits;
+    const size_t items = (size_t)s.S * H * xchunks;
+    if ((rc = s.alloc(&a.x2, (size_t)s.S * d)) || (rc = s.alloc(&a.sa, (size_t)L * s.S * d)) ||
+        (rc = s.alloc(&a.pv, items * 64)) || (rc = s.alloc(&a.psum, items)) || (rc = s.alloc(&a.xmax, items)) ||
+        (rc = s.alloc(&a.flags, (size_t)W)) || (rc = s.alloc(&a.err, 1)))
         return rc;
-    WH_HIP(hipMemsetAsync(a.heads, 0, sizeof(unsigned) * s.S * H, s.st));
+    WH_HIP(hipMemsetAsync(a.xmax, 0, sizeof(uint64_t) * items, s.st));
     WH_HIP(hipMemsetAsync(a.flags, 0, sizeof(unsigned) * W, s.st));
     WH_HIP(hipMemsetAsync(a.err, 0, sizeof(unsigned), s.st));
     a.scale = (float)(1.0 / sqrt(64.0));
