@@ -168,7 +168,8 @@ def test_suppress_nst_greedy_vs_oracle(wh, orc, gpu, prompt):
 
 @contextlib.contextmanager
 def batch_path(on):
-    """The batched persistent forward is chosen when a sequence is created (WHISPER_HIP_BATCH)."""
+    """The batched persistent forward is chosen when a sequence is created
+    (WHISPER_HIP_BATCH, on unless 0)."""
     old = os.environ.get("WHISPER_HIP_BATCH")
     os.environ["WHISPER_HIP_BATCH"] = "1" if on else "0"
     try:
@@ -190,9 +191,9 @@ BATCH_MODELS = [
 
 
 @pytest.mark.parametrize("name,qtype,dims,enc_len", BATCH_MODELS)
-@pytest.mark.parametrize("S", [2, 5, 8])
+@pytest.mark.parametrize("S", [2, 5, 8, 16])
 def test_batched_forward_vs_multikernel_and_oracle(wh, orc, gpu, name, qtype, dims, enc_len, S):
-    """The batched persistent forward (one launch per step for 2..8 states) gives
+    """The batched persistent forward (one launch per step for 2..16 states) gives
     the multi-kernel path's logits (same arithmetic, another summation order) and
     the oracle's, for states at position 0 (its own barrier) and past it."""
     print(f"batched {name} S={S}", flush=True)

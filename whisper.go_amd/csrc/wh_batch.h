@@ -12,7 +12,8 @@ namespace wh {
 namespace batch {
 
 constexpr int NT = 512;              // threads per workgroup (8 waves, two per SIMD)
-constexpr int SMAX = 8;              // streams per launch
+constexpr int SMAX = 16;             // streams per launch
+constexpr int RW = 1;                // GEMV rows per lane group and pass
 constexpr int XBUDGET = 112 * 1024;  // LDS bytes for staged activation matrices [S][cols]
 constexpr int LNMAX = 2048;          // widest LayerNorm whose weights are staged in LDS
 constexpr int CHUNK = 128;           // keys per cross-attention item
@@ -44,6 +45,10 @@ struct BArgs {
 };
 
 constexpr int LMAX = 32;              // layers at most
+
+// Rows of a workgroup's GEMV pass: lane groups of g lanes (32 for widths up to
+// 1024, else 64), 64 / g rows per group.
+constexpr int pass_rows(int d) { return NT / 64 * RW * (d <= 1024 ? 2 : 1); }
 
 // LDS bytes of the kernel: the staged matrix (32 floats per block), its block
 // sums, LayerNorm weight and bias, per-state scalars, a reduction area and the

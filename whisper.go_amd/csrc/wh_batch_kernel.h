@@ -1,5 +1,5 @@
 // Persistent forward of S decoder states (beam hypotheses or independent
-// streams, 2 <= S <= 8) in one cooperative launch per token step
+// streams, 2 <= S <= 16) in one cooperative launch per token step
 // (internal/model/decoder.go:745-993 for every state, reference attention mask).
 //
 // The multi-kernel path runs a step as ~13 launches per layer; each launch costs
@@ -14,7 +14,9 @@
 //   B   LN1(x) -> k,v rows into the KV cache at pos (two thirds of the
 //       workgroups); LN2(x + sa_l) -> cross query rows (the other third)
 //   X   cross attention: workgroup w takes key chunk c of head h of state s
-//       (the host picks the chunk count so that every item has a workgroup);
+//       (the host picks the chunk count so that every item has a workgroup, or
+//       one chunk per head and several heads per workgroup when S * H exceeds
+//       the grid);
 //       scores into LDS, the head maximum from the chunk maxima of the head's
 //       workgroups (a {phase, value} exchange among them, no grid barrier),
 //       fast-exp weights against it and the chunk's partial P.V
@@ -59,26 +61,46 @@ namespace batch {
 constexpr int NWV = NT / 64;
 constexpr int XBLK = XBUDGET / 128;  // staged 32-float blocks, over all states
 constexpr unsigned SPIN_MAX = 1u << 22;
-constexpr int RW = 2;                // rows per lane group and pass
 
 // ---- cross-lane sums ---------------------------------------------------------------
+// DPP lane exchange within rows of 16 lanes
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Wave sum and maximum, left in every lane: quad exchanges, half-row and row
+// mirrors (DPP), then lane swaps across the four rows.
 __device__ __forceinline__ float wsum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp<0x141>(v);  // row_half_mirror
+    v += dpp<0x140>(v);  // row_mirror
+    v += __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
 }
 __device__ __forceinline__ float wmax(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x141>(v));
+    v = fmaxf(v, dpp<0x140>(v));
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return fmaxf(v, __shfl_xor(v, 32, 64));
 }
-// sum over aligned groups of G lanes
+// sum over aligned groups of G lanes (G = 32 or 64), left in every lane of the
+// group: quad exchanges, half-row and row mirrors (DPP), then lane swaps across
+// rows
 template <int G>
 __device__ __forceinline__ float gsum(float v) {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp<0x141>(v);  // row_half_mirror
+    v += dpp<0x140>(v);  // row_mirror
+    v += __shfl_xor(v, 16, 64);
+    if constexpr (G == 64) v += __shfl_xor(v, 32, 64);
     return v;
 }
+// the wave's index, known to be uniform
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
 // ---- global memory ---------------------------------------------------------------------
 // Pointers read from descriptors are generic; typed as global memory, their loads
@@ -341,12 +363,12 @@ __device__ __forceinline__ void stage_ln(int S, int d, Src src, const float *w, 
 // results dropped). A lane takes staged blocks l % G, l % G + G, ... of the row.
 template <int G>
 __device__ __forceinline__ int prow(int P, int r) {
-    return P + (r * (64 / G) + (int)(threadIdx.x & 63) / G) * NWV + (int)(threadIdx.x >> 6);
+    return P + (r * (64 / G) + (int)(threadIdx.x & 63) / G) * NWV + wave_id();
 }
 template <int G>
 __device__ __forceinline__ int pslots(int P, int row1) {
     constexpr int step = (64 / G) * NWV;
-    const int left = row1 - P - (int)(threadIdx.x >> 6);
+    const int left = row1 - P - wave_id();
     return left <= 0 ? 0 : min(RW, (left + step - 1) / step);
 }
 
@@ -359,58 +381,51 @@ __device__ __forceinline__ void load_blks(const MatView &w, int P, int row1, int
 }
 
 // The staged block b of every state against the decoded blocks rb of the lane's
-// rows; every decoded chunk of codes feeds the S states. `valid` false (a lane
-// past the row's last block) leaves acc unchanged.
+// rows: the rows' 32 codes are decoded once, then the states follow one another,
+// each state's eight staged chunks read from LDS together; four partial sums per
+// row keep the FMA chains short. `valid` false (a lane past the row's
+// last block) leaves acc unchanged.
 template <int TYPE>
 __device__ __forceinline__ void dot_blk(const Blk (&rb)[RW], int nr, int S, int b, int nbc, bool valid,
                                         const float4 *xs, const float *sx, float (&acc)[RW][SMAX]) {
-    float qx[RW][SMAX];
+    float q[RW][32];
 #pragma unroll
     for (int r = 0; r < RW; r++)
 #pragma unroll
-        for (int s = 0; s < SMAX; s++) qx[r][s] = 0.0f;
+        for (int k = 0; k < 8; k++) {
+            float c4[4];
+            codes4<TYPE>(rb[r], k, c4);
+            q[r][4 * k] = c4[0];
+            q[r][4 * k + 1] = c4[1];
+            q[r][4 * k + 2] = c4[2];
+            q[r][4 * k + 3] = c4[3];
+        }
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-        // the chunk's codes, made from copies of the raw words that the compiler
-        // cannot see through, so they are not hoisted out for all eight chunks
-        float q[RW][4];
+    for (int s = 0; s < SMAX; s++) {
+        if (s >= S) break;
+        float4 xv[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) xv[k] = xs[slot(s, nbc, b, k)];
+        const float bsum = TYPE == 8 ? 0.0f : sx[s * nbc + b];
 #pragma unroll
         for (int r = 0; r < RW; r++) {
             if (r >= nr) continue;
-            Blk cur = rb[r];
-            asm volatile("" : "+v"(cur.a.x), "+v"(cur.a.y), "+v"(cur.a.z), "+v"(cur.a.w));
-            if constexpr (TYPE == 8) asm volatile("" : "+v"(cur.b.x), "+v"(cur.b.y), "+v"(cur.b.z), "+v"(cur.b.w));
-            if constexpr (TYPE == 6 || TYPE == 7) asm volatile("" : "+v"(cur.h));
-            codes4<TYPE>(cur, k, q[r]);
-        }
+            float p[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < SMAX; s++)
-            if (s < S) {
-                const float4 xv = xs[slot(s, nbc, b, k)];
-#pragma unroll
-                for (int r = 0; r < RW; r++) {
-                    if (r >= nr) continue;
-                    float &c = qx[r][s];
-                    c = __builtin_fmaf(q[r][0], xv.x, c);
-                    c = __builtin_fmaf(q[r][1], xv.y, c);
-                    c = __builtin_fmaf(q[r][2], xv.z, c);
-                    c = __builtin_fmaf(q[r][3], xv.w, c);
-                }
+            for (int k = 0; k < 8; k++) {
+                const float4 x = xv[k];
+                float &c = p[k & 3];
+                c = __builtin_fmaf(q[r][4 * k], x.x, c);
+                c = __builtin_fmaf(q[r][4 * k + 1], x.y, c);
+                c = __builtin_fmaf(q[r][4 * k + 2], x.z, c);
+                c = __builtin_fmaf(q[r][4 * k + 3], x.w, c);
             }
-        // keep the next chunk's LDS reads after these FMAs
+            const float v = bscale<TYPE>(rb[r], (p[0] + p[1]) + (p[2] + p[3]), bsum);
+            acc[r][s] += valid ? v : 0.0f;
+        }
+        // keep the next state's LDS reads after these FMAs
         asm volatile("" ::: "memory");
     }
-#pragma unroll
-    for (int s = 0; s < SMAX; s++)
-        if (s < S) {
-            const float bsum = TYPE == 8 ? 0.0f : sx[s * nbc + b];
-#pragma unroll
-            for (int r = 0; r < RW; r++)
-                if (r < nr) {
-                    const float v = bscale<TYPE>(rb[r], qx[r][s], bsum);
-                    acc[r][s] += valid ? v : 0.0f;
-                }
-        }
 }
 
 // The epilogue operand pre(s, row) of each of the lane's rows for the state the
@@ -654,9 +669,12 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
         gbar(flags, errw, g);
         // ---- X: cross attention; item (state, head, key chunk) on workgroup w ----
         {
-            const int XC = a.xchunks, it = w, klen = (enc_len + XC - 1) / XC;
+            // one item per workgroup when they fit the grid; else XC is 1 and a
+            // workgroup takes whole heads one after another (no exchange to wait on)
+            const int XC = a.xchunks, klen = (enc_len + XC - 1) / XC;
+            for (int it = w; it < S * H * XC; it += W) {
             const int s = it / (H * XC), h = (it / XC) % H, c = it % XC;
-            if (it < S * H * XC && ((amask >> s) & 1u)) {
+            if ((amask >> s) & 1u) {
                 constexpr int KG = 4 * NWV;  // keys per step: 16 lanes per key
                 constexpr int XS = 12;       // steps per batch
                 const int q16 = lane & 15, kq = wv * 4 + (lane >> 4);  // the lane's key of a step
@@ -781,6 +799,8 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
                     for (int i = 0; i < NWV; i++) t += L.red[16 + i];
                     stx(a.psum + it, t);
                 }
+                __syncthreads();  // LDS scores and reduction area free for the next item
+            }
             }
         }
         gbar(flags, errw, g);
@@ -796,13 +816,21 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
                     const size_t b = ((size_t)s * H + (c >> 6)) * XC;
                     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
                     float sum = 0.0f;
+                    // the chunks' loads go out together, then the sums
+                    float4 p4[CMAX];
+                    float ps[CMAX];
 #pragma unroll
-                    for (int i = 0; i < CMAX; i++) {
-                        if (i >= XC) break;
-                        const float4 p4 = ldx4(pvr + (b + i) * 64 + (c & 63));
-                        o.x += p4.x; o.y += p4.y; o.z += p4.z; o.w += p4.w;
-                        sum += ldx(psr + b + i);
-                    }
+                    for (int i = 0; i < CMAX; i++)
+                        if (i < XC) {
+                            p4[i] = ldx4(pvr + (b + i) * 64 + (c & 63));
+                            ps[i] = ldx(psr + b + i);
+                        }
+#pragma unroll
+                    for (int i = 0; i < CMAX; i++)
+                        if (i < XC) {
+                            o.x += p4[i].x; o.y += p4[i].y; o.z += p4[i].z; o.w += p4[i].w;
+                            sum += ps[i];
+                        }
                     const float inv = 1.0f / sum;
                     return make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
                 },

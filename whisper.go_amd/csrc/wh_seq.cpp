@@ -431,15 +431,17 @@ int mega_setup(wh_seq &s) {
     return WH_OK;
 }
 
-// Set up the batched persistent forward for a sequence of 2..8 streams when it
-// is asked for (WHISPER_HIP_BATCH=1; until it outruns the multi-kernel chain it
-// is not the default) and the model fits it (head size 64, width <= 2048, every
-// matrix of the token embedding's quantised type, q/k/v stacked); otherwise the
-// multi-kernel chain serves the steps.
+// Set up the batched persistent forward for a sequence of 2..8 streams (2..16
+// with WHISPER_HIP_BATCH=1; 0 turns it off) when the model fits it (head size 64,
+// width <= 2048, every matrix of the token embedding's quantised type, q/k/v
+// stacked); otherwise the multi-kernel chain serves the steps. Past 8 states the
+// per-lane FMA work of the batched GEMV outgrows the chain's matrix-core GEMV on
+// large models, so the chain is the default there.
 int batch_setup(wh_seq &s) {
     const wh_model &m = *s.m;
     s.batch_ok = false;
-    if (s.S < 2 || s.S > batch::SMAX || !env_int("WHISPER_HIP_BATCH", 0)) return WH_OK;
+    const int want = env_int("WHISPER_HIP_BATCH", -1);
+    if (s.S < 2 || s.S > batch::SMAX || want == 0 || (want < 0 && s.S > 8)) return WH_OK;
     const int d = m.n_state, H = m.n_head, L = m.n_layer;
     if (d / H != 64 || d % 64 != 0 || d > 2048 || !is_quant_type(m.tok.type)) return WH_OK;
     for (const Layer &l : m.layers) {
@@ -454,12 +456,13 @@ int batch_setup(wh_seq &s) {
         return WH_OK;
     const int W = std::min(env_int("WHISPER_HIP_GRID", cus), cus);
     // LDS for the staged [S][d] inputs and the LayerNorm weights; the fc2 column
-    // passes keep <= 16 rows per workgroup; a head has at most CMAX key chunks
-    // cross attention: every (state, head, key chunk) item has a workgroup; a chunk's
-    // scores stay in LDS
+    // passes keep a workgroup's rows within one pass
+    // cross attention: every (state, head, key chunk) item has a workgroup, or one
+    // chunk per head when the heads alone exceed the grid; a chunk's scores stay in LDS
     const int xchunks = std::min(std::max(1, W / (s.S * H)), batch::CMAX);
-    if (W < 8 || (size_t)lds_max < batch::LDS_BYTES || (d + W - 1) / W > 16 || d > batch::LNMAX || L > batch::LMAX ||
-        s.S * (d / 32) > batch::XBUDGET / 128 || s.S * H > W ||
+    if (W < 8 || (size_t)lds_max < batch::LDS_BYTES || (d + W - 1) / W > batch::pass_rows(d) || d > batch::LNMAX ||
+        L > batch::LMAX ||
+        s.S * (d / 32) > batch::XBUDGET / 128 ||
         (size_t)(s.enc_len + xchunks - 1) / xchunks * sizeof(float) > (size_t)batch::XBUDGET)
         return WH_OK;
     std::vector<batch::BLayer> ly(L);
