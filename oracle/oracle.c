@@ -784,8 +784,10 @@ struct or_state {
     float *x, *xln, *q, *k, *v, *attn, *out, *mlp, *kfull, *vfull, *logits_scratch;
 };
 
-/* model/compat.go:31-148 (decoder names only) */
+/* model/compat.go:31-148 */
+static int map_encoder_name(const char *name, char *out, size_t cap);
 static int map_tensor_name(const char *name, char *out, size_t cap) {
+    if (strncmp(name, "encoder.", 8) == 0) return map_encoder_name(name, out, cap);
     static const char *simple[][2] = {
         {"decoder.token_embedding.weight", "model.decoder.embed_tokens.weight"},
         {"decoder.positional_embedding", "model.decoder.embed_positions.weight"},
@@ -1523,4 +1525,307 @@ int or_decode(const or_model *m, const float *enc, int enc_len, const or_decode_
     *out_len = 0;
     if (p->beam_size > 1) return decode_beam(m, enc, enc_len, p, out, cap, out_len);
     return decode_greedy(m, enc, enc_len, p, out, cap, out_len);
+}
+
+
+/* ---- encoder (model/encoder.go) --------------------------------------------- */
+
+/* model/compat.go:31-83, the encoder half of mapTensorName */
+static int map_encoder_name(const char *name, char *out, size_t cap) {
+    static const char *simple[][2] = {
+        {"encoder.conv1.weight", "model.encoder.conv1.weight"},
+        {"encoder.conv1.bias", "model.encoder.conv1.bias"},
+        {"encoder.conv2.weight", "model.encoder.conv2.weight"},
+        {"encoder.conv2.bias", "model.encoder.conv2.bias"},
+        {"encoder.positional_embedding", "model.encoder.embed_positions.weight"},
+        {"encoder.ln_post.weight", "model.encoder.layer_norm.weight"},
+        {"encoder.ln_post.bias", "model.encoder.layer_norm.bias"},
+    };
+    for (size_t i = 0; i < sizeof simple / sizeof simple[0]; i++)
+        if (strcmp(name, simple[i][0]) == 0) { snprintf(out, cap, "%s", simple[i][1]); return 1; }
+    const char *pre = "encoder.blocks.";
+    if (strncmp(name, pre, strlen(pre)) != 0) return 0;
+    const char *rest = name + strlen(pre);
+    char *end;
+    long idx = strtol(rest, &end, 10);
+    if (end == rest || *end != '.') return 0;
+    const char *suf = end + 1;
+    static const char *sm[][2] = {
+        {"attn_ln.weight", "self_attn_layer_norm.weight"}, {"attn_ln.bias", "self_attn_layer_norm.bias"},
+        {"attn.query.weight", "self_attn.q_proj.weight"}, {"attn.query.bias", "self_attn.q_proj.bias"},
+        {"attn.key.weight", "self_attn.k_proj.weight"}, {"attn.value.weight", "self_attn.v_proj.weight"},
+        {"attn.value.bias", "self_attn.v_proj.bias"}, {"attn.out.weight", "self_attn.out_proj.weight"},
+        {"attn.out.bias", "self_attn.out_proj.bias"}, {"mlp_ln.weight", "final_layer_norm.weight"},
+        {"mlp_ln.bias", "final_layer_norm.bias"}, {"mlp.0.weight", "fc1.weight"}, {"mlp.0.bias", "fc1.bias"},
+        {"mlp.2.weight", "fc2.weight"}, {"mlp.2.bias", "fc2.bias"},
+    };
+    for (size_t i = 0; i < sizeof sm / sizeof sm[0]; i++)
+        if (strcmp(suf, sm[i][0]) == 0) { snprintf(out, cap, "model.encoder.layers.%ld.%s", idx, sm[i][1]); return 1; }
+    return 0;
+}
+
+typedef struct {
+    float *attn_lnw, *attn_lnb, *qb, *vb, *ob, *mlp_lnw, *mlp_lnb, *fc1b, *fc2b;
+    omat q, k, v, o, fc1, fc2;
+} oeblock;
+
+struct or_encoder {
+    int n_mels, n_state, n_head, n_layer, n_ctx;
+    int dot_variant, threads, fast_exp;
+    float *conv1w, *conv1b; /* [d, n_mels, 3] */
+    float *conv2w, *conv2b; /* [d, d, 3] */
+    float *pos;             /* [n_ctx, d] */
+    oeblock *blocks;
+    float *ln_postw, *ln_postb;
+};
+
+/* ml/conv.go:19-70: pad = kernel / 2, T' = (T + 2 pad - kernel) / stride + 1;
+ * out[oc, t] = bias[oc] + sum over ic, then k, of in[ic, t stride - pad + k] w[oc, ic, k]
+ * (zero padding), accumulated in that order in float32. Returns T'. */
+int or_conv1d(const float *in, int in_c, int t, const float *w, const float *bias, int out_c, int kernel, int stride,
+              float *out) {
+    const int pad = kernel / 2, tp = (t + 2 * pad - kernel) / stride + 1;
+    for (int oc = 0; oc < out_c; oc++)
+        for (int j = 0; j < tp; j++) {
+            float sum = bias[oc];
+            for (int ic = 0; ic < in_c; ic++)
+                for (int k = 0; k < kernel; k++) {
+                    const int it = j * stride - pad + k;
+                    if (it < 0 || it >= t) continue;
+                    sum += in[(size_t)ic * t + it] * w[((size_t)oc * in_c + ic) * kernel + k];
+                }
+            out[(size_t)oc * tp + j] = sum;
+        }
+    return tp;
+}
+
+/* ml.Transpose of a [a, b, c] tensor by the permutation (i0, i1, i2). */
+static float *transpose3(const float *src, const uint64_t *sh, int i0, int i1, int i2) {
+    const uint64_t n[3] = {sh[0], sh[1], sh[2]};
+    const uint64_t o1 = n[i1], o2 = n[i2];
+    float *o = (float *)malloc(sizeof(float) * (size_t)(n[0] * n[1] * n[2]));
+    for (uint64_t a = 0; a < n[0]; a++)
+        for (uint64_t b = 0; b < n[1]; b++)
+            for (uint64_t c = 0; c < n[2]; c++) {
+                const uint64_t idx[3] = {a, b, c};
+                o[(idx[i0] * o1 + idx[i1]) * o2 + idx[i2]] = src[(a * n[1] + b) * n[2] + c];
+            }
+    return o;
+}
+
+void or_encoder_destroy(or_encoder *e) {
+    if (!e) return;
+    free(e->conv1w); free(e->conv1b); free(e->conv2w); free(e->conv2b); free(e->pos);
+    free(e->ln_postw); free(e->ln_postb);
+    if (e->blocks) {
+        for (int i = 0; i < e->n_layer; i++) {
+            oeblock *b = &e->blocks[i];
+            float *v[] = {b->attn_lnw, b->attn_lnb, b->qb, b->vb, b->ob, b->mlp_lnw, b->mlp_lnb, b->fc1b, b->fc2b};
+            for (size_t j = 0; j < sizeof v / sizeof v[0]; j++) free(v[j]);
+            omat *ms[] = {&b->q, &b->k, &b->v, &b->o, &b->fc1, &b->fc2};
+            for (size_t j = 0; j < sizeof ms / sizeof ms[0]; j++) free(ms[j]->f);
+        }
+        free(e->blocks);
+    }
+    free(e);
+}
+
+/* model/encoder.go:58-263 NewEncoder: hyper-parameters from metadata, else
+ * inferred from the tensors; conv weights in any of the stored orders the
+ * reference accepts; the positional embedding transposed when stored [d, ctx]. */
+or_encoder *or_encoder_create(const or_tensor *t, int n, const or_enc_meta *meta, int dot_variant, int threads) {
+    char msg[300];
+    uint32_t n_head = meta ? meta->n_head : 0, n_layer = meta ? meta->n_layer : 0, n_ctx = meta ? meta->n_ctx : 0;
+    uint32_t n_state = meta ? meta->n_state : 0, n_mels = meta ? meta->n_mels : 0;
+    if (n_layer == 0) {
+        char nm[96];
+        while (1) {
+            snprintf(nm, sizeof nm, "encoder.blocks.%u.attn.query.weight", n_layer);
+            if (!resolve(t, n, nm)) break;
+            n_layer++;
+        }
+    }
+    if (n_state == 0) {
+        const or_tensor *b = resolve(t, n, "encoder.conv1.bias");
+        if (!b) { set_err("model: load tensor \"encoder.conv1.bias\": not found"); return NULL; }
+        if (b->ndim != 1 || b->shape[0] == 0) { set_err("model: encoder: invalid conv1.bias shape"); return NULL; }
+        n_state = (uint32_t)b->shape[0];
+    }
+    const or_tensor *aq = resolve(t, n, "encoder.blocks.0.attn.query.weight");
+    if (aq && aq->ndim == 2 && aq->shape[0] == aq->shape[1] && aq->shape[0] > 0) n_state = (uint32_t)aq->shape[0];
+    const or_tensor *pe = resolve(t, n, "encoder.positional_embedding");
+    if (n_ctx == 0) {
+        if (!pe) { set_err("model: load tensor \"encoder.positional_embedding\": not found"); return NULL; }
+        if (pe->ndim != 2) { set_err("model: encoder: invalid positional embedding shape"); return NULL; }
+        if (pe->shape[0] == n_state && pe->shape[1] != n_state) n_ctx = (uint32_t)pe->shape[1];
+        else n_ctx = (uint32_t)pe->shape[0];
+    }
+    if (n_head == 0) {
+        if (n_state % 64 != 0) {
+            snprintf(msg, sizeof msg, "model: encoder: cannot infer head count from embedding length %u", n_state);
+            set_err(msg);
+            return NULL;
+        }
+        n_head = n_state / 64;
+    }
+    or_encoder *e = (or_encoder *)calloc(1, sizeof *e);
+    e->n_state = (int)n_state; e->n_head = (int)n_head; e->n_layer = (int)n_layer; e->n_ctx = (int)n_ctx;
+    e->dot_variant = dot_variant; e->threads = threads > 0 ? threads : 1; e->fast_exp = 1;
+    const int d = e->n_state;
+    /* conv1: [d, n_mels, 3], or [n_mels, d, 3] (legacy), or [3, n_mels, d] */
+    const or_tensor *c1 = resolve(t, n, "encoder.conv1.weight");
+    if (!c1) { set_err("model: load tensor \"encoder.conv1.weight\": not found"); goto fail; }
+    if (c1->ndim != 3) { set_err("model: encoder: invalid conv1.weight shape"); goto fail; }
+    {
+        float *f = load_f32(c1);
+        if (!f) goto fail;
+        if ((int)c1->shape[0] == d && c1->shape[1] > 0 && c1->shape[2] == 3) {
+            e->conv1w = f;
+            if (n_mels == 0) n_mels = (uint32_t)c1->shape[1];
+        } else if ((int)c1->shape[1] == d && c1->shape[0] > 0 && c1->shape[2] == 3) {
+            e->conv1w = transpose3(f, c1->shape, 1, 0, 2); free(f);
+            if (n_mels == 0) n_mels = (uint32_t)c1->shape[0];
+        } else if (c1->shape[0] == 3 && (int)c1->shape[2] == d && c1->shape[1] > 0) {
+            e->conv1w = transpose3(f, c1->shape, 2, 1, 0); free(f);
+            if (n_mels == 0) n_mels = (uint32_t)c1->shape[1];
+        } else {
+            free(f);
+            set_err("model: encoder: unsupported conv1.weight shape");
+            goto fail;
+        }
+    }
+    e->n_mels = (int)n_mels;
+    if (!(e->conv1b = load_vec(t, n, "encoder.conv1.bias"))) goto fail;
+    {
+        const or_tensor *c2 = resolve(t, n, "encoder.conv2.weight");
+        if (!c2) { set_err("model: load tensor \"encoder.conv2.weight\": not found"); goto fail; }
+        if (c2->ndim != 3) { set_err("model: encoder: invalid conv2.weight shape"); goto fail; }
+        float *f = load_f32(c2);
+        if (!f) goto fail;
+        if ((int)c2->shape[0] == d && (int)c2->shape[1] == d && c2->shape[2] == 3) e->conv2w = f;
+        else if (c2->shape[0] == 3 && (int)c2->shape[1] == d && (int)c2->shape[2] == d) {
+            e->conv2w = transpose3(f, c2->shape, 2, 1, 0); free(f);
+        } else {
+            e->conv2w = transpose3(f, c2->shape, 1, 0, 2); free(f);
+        }
+    }
+    if (!(e->conv2b = load_vec(t, n, "encoder.conv2.bias"))) goto fail;
+    {
+        if (!pe) { set_err("model: load tensor \"encoder.positional_embedding\": not found"); goto fail; }
+        if (pe->ndim != 2) { set_err("model: encoder: invalid positional embedding shape"); goto fail; }
+        float *f = load_f32(pe);
+        if (!f) goto fail;
+        if ((int)pe->shape[0] == d && (int)pe->shape[1] == e->n_ctx) { e->pos = transpose(f, d, e->n_ctx); free(f); }
+        else e->pos = f;
+    }
+    e->blocks = (oeblock *)calloc((size_t)(n_layer ? n_layer : 1), sizeof(oeblock));
+    for (int i = 0; i < e->n_layer; i++) {
+        oeblock *b = &e->blocks[i];
+        char nm[160];
+#define EVEC(field, suf) do { snprintf(nm, sizeof nm, "encoder.blocks.%d." suf, i); if (!(b->field = load_vec(t, n, nm))) goto fail; } while (0)
+#define EMAT(field, suf, r, c) do { snprintf(nm, sizeof nm, "encoder.blocks.%d." suf, i); if (load_mat(t, n, nm, r, c, &b->field)) goto fail; } while (0)
+        EVEC(attn_lnw, "attn_ln.weight"); EVEC(attn_lnb, "attn_ln.bias");
+        EMAT(q, "attn.query.weight", d, d); EVEC(qb, "attn.query.bias");
+        EMAT(k, "attn.key.weight", d, d);
+        EMAT(v, "attn.value.weight", d, d); EVEC(vb, "attn.value.bias");
+        EMAT(o, "attn.out.weight", d, d); EVEC(ob, "attn.out.bias");
+        EVEC(mlp_lnw, "mlp_ln.weight"); EVEC(mlp_lnb, "mlp_ln.bias");
+        EMAT(fc1, "mlp.0.weight", 4 * d, d); EVEC(fc1b, "mlp.0.bias");
+        EMAT(fc2, "mlp.2.weight", d, 4 * d); EVEC(fc2b, "mlp.2.bias");
+#undef EVEC
+#undef EMAT
+    }
+    if (!(e->ln_postw = load_vec(t, n, "encoder.ln_post.weight"))) goto fail;
+    if (!(e->ln_postb = load_vec(t, n, "encoder.ln_post.bias"))) goto fail;
+    return e;
+fail:
+    or_encoder_destroy(e);
+    return NULL;
+}
+
+void or_encoder_set_fast_exp(or_encoder *e, int on) { e->fast_exp = on; }
+
+void or_encoder_hparams(const or_encoder *e, int32_t *o) {
+    o[0] = e->n_mels; o[1] = e->n_state; o[2] = e->n_head; o[3] = e->n_layer; o[4] = e->n_ctx;
+}
+
+static void enc_gemv(const or_encoder *e, const omat *w, const float *a, int rows_a, float *out) {
+    or_gemv(w->type, w->type == 0 ? (const uint8_t *)w->f : w->q, w->rows, w->cols, a, rows_a, out, e->dot_variant,
+            e->threads);
+}
+static void add_bias(float *x, const float *b, int rows, int c) {
+    for (int r = 0; r < rows; r++)
+        for (int j = 0; j < c; j++) x[(size_t)r * c + j] += b[j];
+}
+
+/* model/encoder.go:340-379 runSelfAttn: Q = x Wq^T + bq, K = x Wk^T, V = x Wv^T + bv,
+ * heads [T, H, hd] -> [H, T, hd], SDPA without a mask, back to [T, d], out projection. */
+static void enc_self_attn(const or_encoder *e, const oeblock *b, const float *x, int T, float *out) {
+    const int d = e->n_state, H = e->n_head, hd = d / H;
+    const size_t n = (size_t)T * d;
+    float *Q = (float *)malloc(sizeof(float) * n), *K = (float *)malloc(sizeof(float) * n);
+    float *V = (float *)malloc(sizeof(float) * n), *A = (float *)malloc(sizeof(float) * n);
+    float *qh = (float *)malloc(sizeof(float) * n), *kh = (float *)malloc(sizeof(float) * n);
+    float *vh = (float *)malloc(sizeof(float) * n), *ah = (float *)malloc(sizeof(float) * n);
+    enc_gemv(e, &b->q, x, T, Q); add_bias(Q, b->qb, T, d);
+    enc_gemv(e, &b->k, x, T, K);
+    enc_gemv(e, &b->v, x, T, V); add_bias(V, b->vb, T, d);
+    for (int t = 0; t < T; t++)
+        for (int h = 0; h < H; h++)
+            for (int c = 0; c < hd; c++) {
+                const size_t src = (size_t)t * d + h * hd + c, dst = ((size_t)h * T + t) * hd + c;
+                qh[dst] = Q[src]; kh[dst] = K[src]; vh[dst] = V[src];
+            }
+    or_sdpa(qh, kh, vh, H, T, T, hd, 0, e->fast_exp, ah, NULL);
+    for (int t = 0; t < T; t++)
+        for (int h = 0; h < H; h++)
+            for (int c = 0; c < hd; c++) A[(size_t)t * d + h * hd + c] = ah[((size_t)h * T + t) * hd + c];
+    enc_gemv(e, &b->o, A, T, out); add_bias(out, b->ob, T, d);
+    free(Q); free(K); free(V); free(A); free(qh); free(kh); free(vh); free(ah);
+}
+
+/* model/encoder.go:265-338 Encode: conv stem with GELU, positional embedding,
+ * pre-LN blocks (self-attention, MLP with GELU), final LayerNorm. mel is
+ * [n_mels, T]; out receives [T', d] with T' = T / 2 (T even). Returns T' or -1. */
+int or_encode(const or_encoder *e, const float *mel, int n_mels, int T, float *out) {
+    char msg[200];
+    if (n_mels != e->n_mels) {
+        snprintf(msg, sizeof msg, "model: encoder: mel must be [%d, T], got [%d %d]", e->n_mels, n_mels, T);
+        set_err(msg);
+        return -1;
+    }
+    if (T == 2 * e->n_ctx + 1) T = 2 * e->n_ctx; /* one extra STFT frame: the first 2 n_ctx frames */
+    if (T > 2 * e->n_ctx) {
+        snprintf(msg, sizeof msg, "model: encoder: T=%d > 2*n_audio_ctx=%d", T, 2 * e->n_ctx);
+        set_err(msg);
+        return -1;
+    }
+    const int d = e->n_state;
+    float *c1 = (float *)malloc(sizeof(float) * (size_t)d * (T > 0 ? T : 1));
+    const int t1 = or_conv1d(mel, n_mels, T, e->conv1w, e->conv1b, d, 3, 1, c1);
+    or_gelu(c1, d * t1);
+    const int tp = (t1 + 2 - 3) / 2 + 1;
+    float *c2 = (float *)malloc(sizeof(float) * (size_t)d * (tp > 0 ? tp : 1));
+    or_conv1d(c1, d, t1, e->conv2w, e->conv2b, d, 3, 2, c2);
+    or_gelu(c2, d * tp);
+    float *x = (float *)malloc(sizeof(float) * (size_t)tp * d);
+    for (int t = 0; t < tp; t++)
+        for (int c = 0; c < d; c++) x[(size_t)t * d + c] = c2[(size_t)c * tp + t] + e->pos[(size_t)t * d + c];
+    float *xln = (float *)malloc(sizeof(float) * (size_t)tp * d);
+    float *o = (float *)malloc(sizeof(float) * (size_t)tp * d);
+    float *h = (float *)malloc(sizeof(float) * (size_t)tp * 4 * d);
+    for (int i = 0; i < e->n_layer; i++) {
+        const oeblock *b = &e->blocks[i];
+        or_layernorm(xln, x, b->attn_lnw, b->attn_lnb, tp, d, 1e-5f);
+        enc_self_attn(e, b, xln, tp, o);
+        for (size_t j = 0; j < (size_t)tp * d; j++) x[j] = x[j] + o[j];
+        or_layernorm(xln, x, b->mlp_lnw, b->mlp_lnb, tp, d, 1e-5f);
+        enc_gemv(e, &b->fc1, xln, tp, h); add_bias(h, b->fc1b, tp, 4 * d);
+        or_gelu(h, tp * 4 * d);
+        enc_gemv(e, &b->fc2, h, tp, o); add_bias(o, b->fc2b, tp, d);
+        for (size_t j = 0; j < (size_t)tp * d; j++) x[j] = x[j] + o[j];
+    }
+    or_layernorm(out, x, e->ln_postw, e->ln_postb, tp, d, 1e-5f);
+    free(c1); free(c2); free(x); free(xln); free(o); free(h);
+    return tp;
 }

@@ -98,6 +98,11 @@ typedef struct {
     uint32_t n_head, n_layer, n_ctx, n_state, n_vocab;
 } or_meta;
 
+typedef struct {
+    /* whisper.encoder.* / whisper.audio.mel_count metadata, 0 = absent (encoder.go:63-67) */
+    uint32_t n_head, n_layer, n_ctx, n_state, n_mels;
+} or_enc_meta;
+
 typedef struct or_model or_model;
 typedef struct or_state or_state;
 
@@ -151,6 +156,20 @@ int or_beam_run(const or_model *m, const float *enc, int enc_len, const or_decod
 void or_go_sort_norm(float *norm, int32_t *id, int n);
 
 const char *or_last_error(void);
+
+
+/* ---- encoder (model/encoder.go) ----------------------------------------- */
+typedef struct or_encoder or_encoder;
+or_encoder *or_encoder_create(const or_tensor *t, int n, const or_enc_meta *meta, int dot_variant,
+                              int threads);                         /* model/encoder.go:58-263 */
+void or_encoder_destroy(or_encoder *e);
+void or_encoder_hparams(const or_encoder *e, int32_t *out5);        /* mels,state,head,layer,ctx */
+void or_encoder_set_fast_exp(or_encoder *e, int on);               /* ml/attention.go:18-22 */
+/* Encode (encoder.go:265-338): mel [n_mels, T] -> out [T', d]; returns T' or -1. */
+int or_encode(const or_encoder *e, const float *mel, int n_mels, int T, float *out);
+/* ml/conv.go:19-70; returns T' */
+int or_conv1d(const float *in, int in_c, int t, const float *w, const float *bias, int out_c, int kernel, int stride,
+              float *out);
 
 #ifdef __cplusplus
 }

@@ -25,6 +25,11 @@ class OrMeta(C.Structure):
                 ("n_state", C.c_uint32), ("n_vocab", C.c_uint32)]
 
 
+class OrEncMeta(C.Structure):
+    _fields_ = [("n_head", C.c_uint32), ("n_layer", C.c_uint32), ("n_ctx", C.c_uint32),
+                ("n_state", C.c_uint32), ("n_mels", C.c_uint32)]
+
+
 class OrDecodeParams(C.Structure):
     _fields_ = [("prompt", C.POINTER(C.c_int32)), ("prompt_len", C.c_int32), ("beam_size", C.c_int32),
                 ("temperature", C.c_float), ("logprob_thold", C.c_float), ("no_speech_thold", C.c_float),
@@ -71,6 +76,12 @@ def lib():
             "or_decode": (C.c_int, [P, P, C.c_int, C.POINTER(OrDecodeParams), P, C.c_int, P]),
             "or_beam_run": (C.c_int, [P, P, C.c_int, C.POINTER(OrDecodeParams), P, C.c_int, P, P, P, P, C.c_int]),
             "or_go_sort_norm": (None, [P, P, C.c_int]),
+            "or_encoder_create": (P, [C.POINTER(OrTensor), C.c_int, C.POINTER(OrEncMeta), C.c_int, C.c_int]),
+            "or_encoder_destroy": (None, [P]),
+            "or_encoder_hparams": (None, [P, P]),
+            "or_encoder_set_fast_exp": (None, [P, C.c_int]),
+            "or_encode": (C.c_int, [P, P, C.c_int, C.c_int, P]),
+            "or_conv1d": (C.c_int, [P, C.c_int, C.c_int, P, P, C.c_int, C.c_int, C.c_int, P]),
             "or_last_error": (C.c_char_p, []),
         }
         for name, (res, args) in sig.items():
@@ -305,3 +316,62 @@ class OracleState:
         if lib().or_forward(self.m._h, self._h, _p(enc), enc.shape[0], _p(out)) != 0:
             raise RuntimeError(lib().or_last_error().decode())
         return out
+
+
+def conv1d(x, w, b, stride):
+    """ml/conv.go:19-70 on x [in_c, T], w [out_c, in_c, k], b [out_c] -> [out_c, T']."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    in_c, t = x.shape
+    out_c, _, k = w.shape
+    tp = (t + 2 * (k // 2) - k) // stride + 1
+    out = np.empty((out_c, tp), np.float32)
+    lib().or_conv1d(_p(x), in_c, t, _p(w), _p(b), out_c, k, stride, _p(out))
+    return out
+
+
+def _tensor_array(tensors, keep):
+    arr = (OrTensor * len(tensors))()
+    for i, t in enumerate(tensors):
+        name = t.name.encode()
+        data = np.ascontiguousarray(t.data)
+        keep += [name, data]
+        arr[i].name, arr[i].type, arr[i].ndim = name, t.type, len(t.shape)
+        for j, s in enumerate(t.shape):
+            arr[i].shape[j] = s
+        arr[i].data, arr[i].nbytes = data.ctypes.data, data.size
+    return arr
+
+
+class OracleEncoder:
+    """or_encoder (model/encoder.go) over a tensor table."""
+
+    def __init__(self, tensors, meta=None, dot_variant=1, threads=1):
+        self._keep = []
+        self._arr = _tensor_array(tensors, self._keep)
+        m = OrEncMeta(**(meta or {}))
+        self._h = lib().or_encoder_create(self._arr, len(tensors), C.byref(m), dot_variant, threads)
+        if not self._h:
+            raise RuntimeError(lib().or_last_error().decode())
+        hp = np.zeros(5, np.int32)
+        lib().or_encoder_hparams(self._h, _p(hp))
+        self.n_mels, self.n_state, self.n_head, self.n_layer, self.n_ctx = (int(v) for v in hp)
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().or_encoder_destroy(self._h)
+            self._h = None
+
+    def set_fast_exp(self, on):
+        lib().or_encoder_set_fast_exp(self._h, int(on))
+
+    def encode(self, mel):
+        """mel [n_mels, T] -> encoder output [T', n_state] (T' = T / 2)."""
+        mel = np.ascontiguousarray(mel, np.float32)
+        nm, t = mel.shape
+        out = np.empty((max(1, (min(t, 2 * self.n_ctx) + 1) // 2), self.n_state), np.float32)
+        tp = lib().or_encode(self._h, _p(mel), nm, t, _p(out))
+        if tp < 0:
+            raise RuntimeError(lib().or_last_error().decode())
+        return out[:tp]

@@ -58,7 +58,7 @@ def tensor_specs(n_vocab, d, n_layer, n_ctx):
 
 
 def is_ln_gain(name):
-    return name.endswith("_ln.weight") or name == "decoder.ln.weight"
+    return name.endswith("_ln.weight") or name in ("decoder.ln.weight", "encoder.ln_post.weight")
 
 
 def gen_f32(config, name, shape, std=0.02):
@@ -98,6 +98,57 @@ def make_decoder(config="tiny.en", qtype=8, dims=None, std=0.02):
             out.append(Tensor(name, 0, shape, x))
     meta = dict(n_head=H, n_layer=L, n_ctx=ctx, n_state=d, n_vocab=V)
     return out, meta
+
+
+# encoder: (n_mels, n_state, n_head, n_layer, n_audio_ctx)
+ENC_CONFIGS = {
+    "tiny.en": (80, 384, 6, 4, 1500),
+    "base": (80, 512, 8, 6, 1500),
+    "small": (80, 768, 12, 12, 1500),
+    "medium": (80, 1024, 16, 24, 1500),
+    "large-v3": (128, 1280, 20, 32, 1500),
+}
+
+
+def encoder_specs(n_mels, d, n_layer, n_ctx):
+    """(name, shape) of every encoder tensor (internal/model/encoder.go:58-263)."""
+    specs = [("encoder.conv1.weight", (d, n_mels, 3)), ("encoder.conv1.bias", (d,)),
+             ("encoder.conv2.weight", (d, d, 3)), ("encoder.conv2.bias", (d,)),
+             ("encoder.positional_embedding", (n_ctx, d))]
+    for i in range(n_layer):
+        p = f"encoder.blocks.{i}."
+        specs += [(p + "attn_ln.weight", (d,)), (p + "attn_ln.bias", (d,)),
+                  (p + "attn.query.weight", (d, d)), (p + "attn.query.bias", (d,)),
+                  (p + "attn.key.weight", (d, d)),
+                  (p + "attn.value.weight", (d, d)), (p + "attn.value.bias", (d,)),
+                  (p + "attn.out.weight", (d, d)), (p + "attn.out.bias", (d,)),
+                  (p + "mlp_ln.weight", (d,)), (p + "mlp_ln.bias", (d,)),
+                  (p + "mlp.0.weight", (4 * d, d)), (p + "mlp.0.bias", (4 * d,)),
+                  (p + "mlp.2.weight", (d, 4 * d)), (p + "mlp.2.bias", (d,))]
+    specs += [("encoder.ln_post.weight", (d,)), ("encoder.ln_post.bias", (d,))]
+    return specs
+
+
+def make_encoder(config="tiny.en", qtype=8, dims=None, std=0.02):
+    """Synthetic encoder tensors quantised with the cmd/quantize rule (the conv
+    weights and the block LN gains too, as the rule quantises every ".weight"
+    whose name has neither "norm" nor ".ln"). dims overrides ENC_CONFIGS[config]
+    with (n_mels, n_state, n_head, n_layer, n_audio_ctx). Returns (tensors, meta)."""
+    M, d, H, L, ctx = dims if dims is not None else ENC_CONFIGS[config]
+    out = []
+    for name, shape in encoder_specs(M, d, L, ctx):
+        x = gen_f32(config, name, shape, std)
+        if qtype != 0 and quant.should_quantize(name) and x.size % 32 == 0:
+            out.append(Tensor(name, qtype, shape, quant.quantize(qtype, x)))
+        else:
+            out.append(Tensor(name, 0, shape, x))
+    meta = dict(n_head=H, n_layer=L, n_ctx=ctx, n_state=d, n_mels=M)
+    return out, meta
+
+
+def mel_input(config, n_mels, T=3000, stream=0):
+    """Synthetic log-mel input [n_mels, T] ~ N(0, 0.5), seeded per stream."""
+    return (0.5 * rng_for(config, f"mel/{stream}").standard_normal((n_mels, T))).astype(np.float32)
 
 
 def stream_prompts(n_streams=16, seed=16, min_len=4, max_len=224):
