@@ -153,6 +153,36 @@ int wh_model_weight_bytes(const wh_model *m, uint64_t *bytes);
  * mask over the KV cache (opt-in deviation). */
 int wh_model_set_attention_mode(wh_model *m, int32_t mode);
 
+/* ---- Encoder: the model.Encoder interface (internal/model/encoder.go) ------ */
+/* GGUF metadata the encoder loader reads (internal/model/encoder.go:63-67); 0 = absent. */
+typedef struct {
+    uint32_t n_head;  /* whisper.encoder.attention.head_count */
+    uint32_t n_layer; /* whisper.encoder.layer_count */
+    uint32_t n_ctx;   /* whisper.encoder.context_length (audio frames after the stride-2 conv) */
+    uint32_t n_state; /* whisper.encoder.embedding_length */
+    uint32_t n_mels;  /* whisper.audio.mel_count / whisper.n_mels */
+} wh_enc_meta;
+
+typedef struct wh_encoder wh_encoder;
+/* Build an encoder from a tensor table and upload every weight to HBM once;
+ * replaces NewEncoder (internal/model/encoder.go:58-263): hyper-parameters from
+ * meta, else inferred from the tensors; conv weights in any stored order the
+ * reference accepts; HF alias names (internal/model/compat.go:31-83). */
+int wh_encoder_create(const wh_tensor *tensors, int32_t n, const wh_enc_meta *meta, int32_t device,
+                      wh_encoder **out);
+/* Same, reading a GGUF v2/v3 file. */
+int wh_encoder_load_gguf(const char *path, int32_t device, wh_encoder **out);
+int wh_encoder_destroy(wh_encoder *e);
+/* out5 = {n_mels, n_state, n_head, n_layer, n_ctx}. */
+int wh_encoder_hparams(const wh_encoder *e, int32_t *out5);
+/* Encode (internal/model/encoder.go:265-338): mel is host float32 [n_mels, T]
+ * row-major; T = 2 n_ctx + 1 keeps the first n_mels * 2 n_ctx values, T > 2 n_ctx
+ * is WH_ERR_INVALID. The output [T', n_state] (T' = (T + 1) / 2) goes to out,
+ * which holds out_cap rows; *out_rows = T'. cancel (may be NULL) is polled
+ * between blocks (WH_ERR_CANCELLED). */
+int wh_encode(const wh_encoder *e, const float *mel, int32_t n_mels, int32_t T, float *out, int32_t out_cap,
+              int32_t *out_rows, const volatile int32_t *cancel);
+
 /* ---- Decode: the model.Decoder interface (internal/model/interfaces.go:22-25) */
 /* Mirrors model.DecoderParams (internal/model/interfaces.go:76-90); the
  * fields the reference's decoder does not read are omitted. */

@@ -6,8 +6,8 @@ reference's decoder interface plus fixture tooling. Import it by path (the
 directory name contains a dot), e.g. via __graft_entry__.load_package().
 """
 from . import native, quant, synth  # noqa: F401
-from .model import (CancelledError, DecoderParams, HIPDecoder, Segment, Sequence, ShapeMismatchError,  # noqa: F401
-                    TokenData, tokens_to_segments)
+from .model import (CancelledError, DecoderParams, HIPDecoder, HIPEncoder, Segment, Sequence,  # noqa: F401
+                    ShapeMismatchError, TokenData, tokens_to_segments)
 
-__all__ = ["native", "quant", "synth", "HIPDecoder", "Sequence", "DecoderParams", "Segment", "TokenData",
+__all__ = ["native", "quant", "synth", "HIPDecoder", "HIPEncoder", "Sequence", "DecoderParams", "Segment", "TokenData",
            "ShapeMismatchError", "CancelledError", "tokens_to_segments"]

@@ -19,8 +19,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # the slowest first: the five instantiations of the batched persistent forward
 SOURCES = ["wh_batch_q4_0.hip", "wh_batch_q4_1.hip", "wh_batch_q5_0.hip", "wh_batch_q5_1.hip", "wh_batch_q8_0.hip",
-           "wh_mega.hip", "wh_kernels.hip", "wh_batch.hip", "wh_noalloc.hip", "wh_seq.cpp", "wh_quant.cpp",
-           "wh_model.cpp", "wh_api.cpp"]
+           "wh_mega.hip", "wh_kernels.hip", "wh_batch.hip", "wh_noalloc.hip", "wh_encoder.hip", "wh_seq.cpp",
+           "wh_quant.cpp", "wh_model.cpp", "wh_encoder.cpp", "wh_api.cpp"]
 CFLAGS = [
     "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-x", "hip",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -24,6 +24,11 @@ int fail(int code, const std::string &msg) {
 
 int model_create(const wh_tensor *tensors, int32_t n, const wh_meta *meta, int32_t device, wh_model **out);
 void model_free(wh_model *m);
+int encoder_create(const wh_tensor *tensors, int32_t n, const wh_enc_meta *meta, int32_t device, wh_encoder **out);
+void encoder_free(wh_encoder *e);
+int encoder_hparams(const wh_encoder *e, int32_t *o);
+int encode(const wh_encoder *e, const float *mel, int32_t n_mels, int32_t T, float *out, int32_t out_cap,
+           int32_t *out_rows, const volatile int32_t *cancel);
 int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t enc_len, int32_t enc_dim, int32_t shared,
                wh_seq **out);
 int seq_set_tokens(wh_seq *s, int32_t i, const int32_t *tokens, int32_t n, int32_t reset_kv);
@@ -88,9 +93,25 @@ struct Reader {
 
 }  // namespace
 
-int model_load_gguf(const char *path, int32_t device, wh_model **out) {
-    if (!path || !out) return fail(WH_ERR_INVALID, "gguf: open: null argument");
-    *out = nullptr;
+// A GGUF v2/v3 file mapped read-only (gguf.go:52-135): the tensor table points
+// into the mapping, the u32 metadata values are kept by key.
+struct GgufMap {
+    void *mp = nullptr;
+    size_t size = 0;
+    std::vector<std::string> names;
+    std::vector<wh_tensor> table;
+    std::map<std::string, uint32_t> u32;
+    uint32_t get(const char *k) const {
+        auto it = u32.find(k);
+        return it == u32.end() ? 0u : it->second;
+    }
+    ~GgufMap() {
+        if (mp) munmap(mp, size);
+    }
+};
+
+int gguf_map(const char *path, GgufMap &g) {
+    if (!path) return fail(WH_ERR_INVALID, "gguf: open: null argument");
     int fd = open(path, O_RDONLY);
     if (fd < 0) return fail(WH_ERR_INVALID, std::string("gguf: open: ") + path + ": " + std::strerror(errno));
     struct stat stt;
@@ -99,24 +120,25 @@ int model_load_gguf(const char *path, int32_t device, wh_model **out) {
     void *mp = mmap(nullptr, size, PROT_READ, MAP_PRIVATE, fd, 0);
     close(fd);
     if (mp == MAP_FAILED) return fail(WH_ERR_INVALID, "gguf: mmap failed");
-    struct Unmap { void *p; size_t n; ~Unmap() { munmap(p, n); } } unmap{mp, size};
+    g.mp = mp;
+    g.size = size;
     Reader r{(const uint8_t *)mp, (const uint8_t *)mp + size};
     if (std::memcmp(r.p, "GGUF", 4) != 0) return fail(WH_ERR_INVALID, "gguf: invalid magic");
     r.p += 4;
     uint32_t version = r.get<uint32_t>();
     if (version != 2 && version != 3) return fail(WH_ERR_UNSUPPORTED, "gguf: unsupported version: " + std::to_string(version));
     uint64_t nt = r.get<uint64_t>(), nm = r.get<uint64_t>();
-    std::map<std::string, uint32_t> u32;
     for (uint64_t i = 0; i < nm && r.ok; i++) {
         std::string key = r.str();
         uint32_t t = r.get<uint32_t>();
-        r.skip(t, &u32, key);
+        r.skip(t, &g.u32, key);
     }
     if (!r.ok) return fail(WH_ERR_INVALID, "gguf: metadata: truncated");
-    struct Desc { std::string name; std::vector<uint64_t> shape; uint32_t type; uint64_t off; };
+    struct Desc { std::vector<uint64_t> shape; uint32_t type; uint64_t off; };
     std::vector<Desc> descs(nt);
+    g.names.resize(nt);
     for (uint64_t i = 0; i < nt && r.ok; i++) {
-        descs[i].name = r.str();
+        g.names[i] = r.str();
         uint32_t nd = r.get<uint32_t>();
         if (nd > 4) return fail(WH_ERR_INVALID, "gguf: tensor: too many dimensions");
         for (uint32_t j = 0; j < nd; j++) descs[i].shape.push_back(r.get<uint64_t>());
@@ -125,15 +147,15 @@ int model_load_gguf(const char *path, int32_t device, wh_model **out) {
     }
     if (!r.ok) return fail(WH_ERR_INVALID, "gguf: tensor info: truncated");
     uint64_t align = 32;
-    auto ai = u32.find("general.alignment");
-    if (ai != u32.end() && ai->second > 0) align = ai->second;
+    auto ai = g.u32.find("general.alignment");
+    if (ai != g.u32.end() && ai->second > 0) align = ai->second;
     const uint64_t pos = (uint64_t)(r.p - (const uint8_t *)mp);
     const uint64_t data_start = (pos + align - 1) / align * align;
-    std::vector<wh_tensor> table(nt);
+    g.table.resize(nt);
     for (uint64_t i = 0; i < nt; i++) {
-        wh_tensor &t = table[i];
+        wh_tensor &t = g.table[i];
         const Desc &d = descs[i];
-        t.name = d.name.c_str();
+        t.name = g.names[i].c_str();
         t.type = d.type;
         t.ndim = (uint32_t)d.shape.size();
         uint64_t n = 1;
@@ -142,15 +164,41 @@ int model_load_gguf(const char *path, int32_t device, wh_model **out) {
         t.data = (const uint8_t *)mp + data_start + d.off;
         t.nbytes = (data_start + d.off <= size) ? std::min<uint64_t>(bytes, size - data_start - d.off) : 0;
     }
+    return WH_OK;
+}
+
+int model_load_gguf(const char *path, int32_t device, wh_model **out) {
+    if (!path || !out) return fail(WH_ERR_INVALID, "gguf: open: null argument");
+    *out = nullptr;
+    GgufMap g;
+    int rc = gguf_map(path, g);
+    if (rc) return rc;
     wh_meta meta{};
-    auto get = [&](const char *k) { auto it = u32.find(k); return it == u32.end() ? 0u : it->second; };
-    meta.n_head = get("whisper.decoder.attention.head_count");
-    meta.n_layer = get("whisper.decoder.layer_count");
-    meta.n_ctx = get("whisper.decoder.context_length");
-    meta.n_state = get("whisper.decoder.embedding_length");
-    meta.n_vocab = get("whisper.vocab.size");
-    if (!meta.n_vocab) meta.n_vocab = get("whisper.n_vocab");
-    return model_create(table.data(), (int32_t)table.size(), &meta, device, out);
+    meta.n_head = g.get("whisper.decoder.attention.head_count");
+    meta.n_layer = g.get("whisper.decoder.layer_count");
+    meta.n_ctx = g.get("whisper.decoder.context_length");
+    meta.n_state = g.get("whisper.decoder.embedding_length");
+    meta.n_vocab = g.get("whisper.vocab.size");
+    if (!meta.n_vocab) meta.n_vocab = g.get("whisper.n_vocab");
+    return model_create(g.table.data(), (int32_t)g.table.size(), &meta, device, out);
+}
+
+// NewEncoder over a GGUF file (encoder.go:58-67: whisper.encoder.* metadata,
+// the mel band count under either key).
+int encoder_load_gguf(const char *path, int32_t device, wh_encoder **out) {
+    if (!path || !out) return fail(WH_ERR_INVALID, "gguf: open: null argument");
+    *out = nullptr;
+    GgufMap g;
+    int rc = gguf_map(path, g);
+    if (rc) return rc;
+    wh_enc_meta meta{};
+    meta.n_head = g.get("whisper.encoder.attention.head_count");
+    meta.n_layer = g.get("whisper.encoder.layer_count");
+    meta.n_ctx = g.get("whisper.encoder.context_length");
+    meta.n_state = g.get("whisper.encoder.embedding_length");
+    meta.n_mels = g.get("whisper.audio.mel_count");
+    if (!meta.n_mels) meta.n_mels = g.get("whisper.n_mels");
+    return encoder_create(g.table.data(), (int32_t)g.table.size(), &meta, device, out);
 }
 
 }  // namespace wh
@@ -316,6 +364,22 @@ int wh_model_create(const wh_tensor *tensors, int32_t n, const wh_meta *meta, in
     return model_create(tensors, n, meta, device, out);
 }
 int wh_model_load_gguf(const char *path, int32_t device, wh_model **out) { return model_load_gguf(path, device, out); }
+int wh_encoder_create(const wh_tensor *tensors, int32_t n, const wh_enc_meta *meta, int32_t device,
+                      wh_encoder **out) {
+    return encoder_create(tensors, n, meta, device, out);
+}
+int wh_encoder_load_gguf(const char *path, int32_t device, wh_encoder **out) {
+    return encoder_load_gguf(path, device, out);
+}
+int wh_encoder_destroy(wh_encoder *e) {
+    encoder_free(e);
+    return WH_OK;
+}
+int wh_encoder_hparams(const wh_encoder *e, int32_t *out5) { return encoder_hparams(e, out5); }
+int wh_encode(const wh_encoder *e, const float *mel, int32_t n_mels, int32_t T, float *out, int32_t out_cap,
+              int32_t *out_rows, const volatile int32_t *cancel) {
+    return encode(e, mel, n_mels, T, out, out_cap, out_rows, cancel);
+}
 int wh_model_destroy(wh_model *m) {
     model_free(m);
     return WH_OK;

@@ -138,8 +138,14 @@ struct CrossBufs {
 };
 int launch_cross_attn(const float *q, const float *const *kbase, const float *const *vbase, const int32_t *active,
                       float *out, int S, int H, int hd, int enc_len, const CrossBufs &b, hipStream_t st);
+// out[T, rows] = enc[T, cols] . w^T (+ bias); gelu: gelu of that; res: res + that.
 int launch_cross_gemm(const DevMat &w, const float *enc, int enc_len, const float *bias, float *out,
-                      hipStream_t st);
+                      hipStream_t st, int gelu = 0, const float *res = nullptr);
+// encoder kernels (wh_encoder.hip)
+int launch_im2col(const float *in, int64_t sc, int64_t st, int cin, int tin, int stride, int tout, int K, float *out,
+                  hipStream_t s);
+int launch_gelu_add(float *x, const float *pos, int64_t n, hipStream_t s);
+int launch_enc_attn(const float *Q, const float *K, const float *V, int T, int d, int H, float *out, hipStream_t s);
 struct SampleBufs {
     float *cur;          // [S][V] penalised logits
     float *part_val;     // [S][P]

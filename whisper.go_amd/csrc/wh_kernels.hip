@@ -1316,7 +1316,9 @@ __device__ __forceinline__ void dequant8(const MatView &m, int r, int b, int g, 
 }
 
 template <int TYPE>
-__global__ __launch_bounds__(256) void k_cross_gemm(MatView w, const float *E, int T, const float *bias, float *C) {
+// Epilogue: v = acc + bias; gelu: C = gelu(v); res: C = res + v (res may alias C).
+__global__ __launch_bounds__(256) void k_cross_gemm(MatView w, const float *E, int T, const float *bias, float *C,
+                                                    int gelu, const float *res) {
     __shared__ float Es[64][33];  // [frame][k]; the padding keeps the operand reads conflict-free
     __shared__ float Ws[64][33];  // [row][k]
     const int t0 = blockIdx.y * 64, r0 = blockIdx.x * 64;
@@ -1372,7 +1374,11 @@ __global__ __launch_bounds__(256) void k_cross_gemm(MatView w, const float *E, i
 #pragma unroll
     for (int i = 0; i < 16; i++) {
         const int t = t0 + wt + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        if (t < T && r < w.rows) C[(size_t)t * w.rows + r] = bias ? acc[i] + bb : acc[i];
+        if (t < T && r < w.rows) {
+            const size_t o = (size_t)t * w.rows + r;
+            const float v = bias ? acc[i] + bb : acc[i];
+            C[o] = gelu ? gelu_ref(v) : res ? res[o] + v : v;
+        }
     }
 }
 
@@ -1380,7 +1386,8 @@ __global__ __launch_bounds__(256) void k_cross_gemm(MatView w, const float *E, i
 // number of blocks (small test models): one 32-column block per K-step,
 // element-wise dequantisation, columns past the row end read as zero.
 template <int TYPE>
-__global__ __launch_bounds__(256) void k_cross_gemm_simt(MatView w, const float *E, int T, const float *bias, float *C) {
+__global__ __launch_bounds__(256) void k_cross_gemm_simt(MatView w, const float *E, int T, const float *bias, float *C,
+                                                         int gelu, const float *res) {
     __shared__ float Es[32][64 + 4];
     __shared__ float Ws[32][64 + 4];
     const int t0 = blockIdx.y * 64, r0 = blockIdx.x * 64;
@@ -1422,35 +1429,40 @@ __global__ __launch_bounds__(256) void k_cross_gemm_simt(MatView w, const float 
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             int r = r0 + tx * 4 + j;
-            if (r < w.rows) C[(size_t)t * w.rows + r] = bias ? acc[i][j] + bias[r] : acc[i][j];
+            if (r < w.rows) {
+                const size_t o = (size_t)t * w.rows + r;
+                const float v = bias ? acc[i][j] + bias[r] : acc[i][j];
+                C[o] = gelu ? gelu_ref(v) : res ? res[o] + v : v;
+            }
         }
     }
 }
 
-int launch_cross_gemm(const DevMat &w, const float *enc, int enc_len, const float *bias, float *out, hipStream_t st) {
+int launch_cross_gemm(const DevMat &w, const float *enc, int enc_len, const float *bias, float *out, hipStream_t st,
+                      int gelu, const float *res) {
     MatView v = view_of(w);
     dim3 grid((w.rows + 63) / 64, (enc_len + 63) / 64);
     if (w.cols % 32 != 0 || (((uintptr_t)enc) & 15) != 0) {
         // a partial last block or unaligned frame rows: the vector-unit GEMM
         switch (w.type) {
-        case 0: hipLaunchKernelGGL(k_cross_gemm_simt<0>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
-        case 2: hipLaunchKernelGGL(k_cross_gemm_simt<2>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
-        case 3: hipLaunchKernelGGL(k_cross_gemm_simt<3>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
-        case 6: hipLaunchKernelGGL(k_cross_gemm_simt<6>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
-        case 7: hipLaunchKernelGGL(k_cross_gemm_simt<7>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
-        case 8: hipLaunchKernelGGL(k_cross_gemm_simt<8>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
+        case 0: hipLaunchKernelGGL(k_cross_gemm_simt<0>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
+        case 2: hipLaunchKernelGGL(k_cross_gemm_simt<2>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
+        case 3: hipLaunchKernelGGL(k_cross_gemm_simt<3>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
+        case 6: hipLaunchKernelGGL(k_cross_gemm_simt<6>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
+        case 7: hipLaunchKernelGGL(k_cross_gemm_simt<7>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
+        case 8: hipLaunchKernelGGL(k_cross_gemm_simt<8>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
         default: return fail(WH_ERR_UNSUPPORTED, "cross gemm: unsupported type");
         }
         WH_HIP(hipGetLastError());
         return WH_OK;
     }
     switch (w.type) {
-    case 0: hipLaunchKernelGGL(k_cross_gemm<0>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
-    case 2: hipLaunchKernelGGL(k_cross_gemm<2>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
-    case 3: hipLaunchKernelGGL(k_cross_gemm<3>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
-    case 6: hipLaunchKernelGGL(k_cross_gemm<6>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
-    case 7: hipLaunchKernelGGL(k_cross_gemm<7>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
-    case 8: hipLaunchKernelGGL(k_cross_gemm<8>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out); break;
+    case 0: hipLaunchKernelGGL(k_cross_gemm<0>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
+    case 2: hipLaunchKernelGGL(k_cross_gemm<2>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
+    case 3: hipLaunchKernelGGL(k_cross_gemm<3>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
+    case 6: hipLaunchKernelGGL(k_cross_gemm<6>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
+    case 7: hipLaunchKernelGGL(k_cross_gemm<7>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
+    case 8: hipLaunchKernelGGL(k_cross_gemm<8>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
     default: return fail(WH_ERR_UNSUPPORTED, "cross gemm: unsupported type");
     }
     WH_HIP(hipGetLastError());

@@ -11,13 +11,52 @@
 #include <vector>
 
 #include "wh_internal.h"
+#include "wh_load.h"
 
 namespace wh {
 
 namespace {
 
-// HF-style aliases of the decoder tensors (internal/model/compat.go:31-148).
+// HF-style aliases of the encoder tensors (internal/model/compat.go:31-83).
+std::string map_encoder_name(const std::string &name) {
+    static const std::map<std::string, std::string> simple = {
+        {"encoder.conv1.weight", "model.encoder.conv1.weight"},
+        {"encoder.conv1.bias", "model.encoder.conv1.bias"},
+        {"encoder.conv2.weight", "model.encoder.conv2.weight"},
+        {"encoder.conv2.bias", "model.encoder.conv2.bias"},
+        {"encoder.positional_embedding", "model.encoder.embed_positions.weight"},
+        {"encoder.ln_post.weight", "model.encoder.layer_norm.weight"},
+        {"encoder.ln_post.bias", "model.encoder.layer_norm.bias"},
+    };
+    auto it = simple.find(name);
+    if (it != simple.end()) return it->second;
+    static const std::string pre = "encoder.blocks.";
+    if (name.compare(0, pre.size(), pre) != 0) return "";
+    size_t dot = name.find('.', pre.size());
+    if (dot == std::string::npos || dot == pre.size()) return "";
+    const std::string idx = name.substr(pre.size(), dot - pre.size());
+    for (char c : idx)
+        if (c < '0' || c > '9') return "";
+    static const std::map<std::string, std::string> suffix = {
+        {"attn_ln.weight", "self_attn_layer_norm.weight"}, {"attn_ln.bias", "self_attn_layer_norm.bias"},
+        {"attn.query.weight", "self_attn.q_proj.weight"},  {"attn.query.bias", "self_attn.q_proj.bias"},
+        {"attn.key.weight", "self_attn.k_proj.weight"},    {"attn.value.weight", "self_attn.v_proj.weight"},
+        {"attn.value.bias", "self_attn.v_proj.bias"},      {"attn.out.weight", "self_attn.out_proj.weight"},
+        {"attn.out.bias", "self_attn.out_proj.bias"},      {"mlp_ln.weight", "final_layer_norm.weight"},
+        {"mlp_ln.bias", "final_layer_norm.bias"},          {"mlp.0.weight", "fc1.weight"},
+        {"mlp.0.bias", "fc1.bias"},                        {"mlp.2.weight", "fc2.weight"},
+        {"mlp.2.bias", "fc2.bias"},
+    };
+    auto s = suffix.find(name.substr(dot + 1));
+    if (s == suffix.end()) return "";
+    return "model.encoder.layers." + idx + "." + s->second;
+}
+
+}  // namespace
+
+// HF-style aliases of the decoder and encoder tensors (internal/model/compat.go:31-148).
 std::string map_tensor_name(const std::string &name) {
+    if (name.compare(0, 8, "encoder.") == 0) return map_encoder_name(name);
     static const std::map<std::string, std::string> simple = {
         {"decoder.token_embedding.weight", "model.decoder.embed_tokens.weight"},
         {"decoder.positional_embedding", "model.decoder.embed_positions.weight"},
@@ -52,17 +91,14 @@ std::string map_tensor_name(const std::string &name) {
     return "model.decoder.layers." + idx + "." + s->second;
 }
 
-struct Table {
-    std::map<std::string, const wh_tensor *> byname;
-    const wh_tensor *resolve(const std::string &name) const {  // compat.go:15-29
-        auto it = byname.find(name);
-        if (it != byname.end()) return it->second;
-        std::string alt = map_tensor_name(name);
-        if (alt.empty()) return nullptr;
-        it = byname.find(alt);
-        return it == byname.end() ? nullptr : it->second;
-    }
-};
+const wh_tensor *Table::resolve(const std::string &name) const {  // compat.go:15-29
+    auto it = byname.find(name);
+    if (it != byname.end()) return it->second;
+    std::string alt = map_tensor_name(name);
+    if (alt.empty()) return nullptr;
+    it = byname.find(alt);
+    return it == byname.end() ? nullptr : it->second;
+}
 
 uint64_t numel(const wh_tensor *t) {
     uint64_t n = 1;
@@ -84,17 +120,13 @@ int load_f32(const wh_tensor *t, std::vector<float> &out) {
     return dequantize_host(t->type, (const uint8_t *)t->data, n, out.data());
 }
 
-struct VecArena {
-    std::vector<float> host;
-    std::vector<std::pair<float **, size_t>> fix;  // pointer slot, offset in floats
-    int add(const std::vector<float> &v, float **slot) {
-        size_t off = host.size();
-        host.insert(host.end(), v.begin(), v.end());
-        while (host.size() % 64) host.push_back(0.0f);  // 256-byte alignment per vector
-        fix.emplace_back(slot, off);
-        return WH_OK;
-    }
-};
+int VecArena::add(const std::vector<float> &v, float **slot) {
+    size_t off = host.size();
+    host.insert(host.end(), v.begin(), v.end());
+    while (host.size() % 64) host.push_back(0.0f);  // 256-byte alignment per vector
+    fix.emplace_back(slot, off);
+    return WH_OK;
+}
 
 // internal/model/compat.go:247-270 loadMatWeightAuto: a quantised 2-D tensor
 // of the wanted shape is uploaded as is; anything else is dequantised to f32
@@ -139,6 +171,8 @@ int load_vector(const Table &tab, const std::string &name, VecArena &arena, floa
                                         std::to_string(min_len));
     return arena.add(f, slot);
 }
+
+namespace {
 
 // Row constants of a LayerNorm folded into the matrix w that reads its output:
 // c = w·g (g the LayerNorm weight) and e = w·b + bias, by the quantised GEMV.

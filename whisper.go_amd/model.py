@@ -118,6 +118,54 @@ def _tensor_table(tensors):
     return arr, keep
 
 
+class HIPEncoder:
+    """An encoder whose weights live in HBM (WhisperEncoder: NewEncoder + Encode,
+    internal/model/encoder.go:58-338)."""
+
+    def __init__(self, tensors=None, meta=None, device=0, gguf_path=None):
+        h = C.c_void_p()
+        if gguf_path is not None:
+            rc = lib().wh_encoder_load_gguf(gguf_path.encode(), device, C.byref(h))
+        else:
+            arr, keep = _tensor_table(tensors)
+            m = native.WhEncMeta(**(meta or {}))
+            rc = lib().wh_encoder_create(arr, len(tensors), C.byref(m), device, C.byref(h))
+            del keep
+        if rc != native.WH_OK:
+            _raise(rc)
+        self._h = h
+        hp = (C.c_int32 * 5)()
+        check(lib().wh_encoder_hparams(h, hp))
+        self.n_mels, self.n_state, self.n_head, self.n_layer, self.n_ctx = list(hp)
+
+    @classmethod
+    def from_gguf(cls, path, device=0):
+        return cls(gguf_path=path, device=device)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().wh_encoder_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def encode(self, mel, cancel: Optional[C.c_int32] = None):
+        """mel [n_mels, T] float32 -> encoder output [T', n_state] (T' = (T + 1) / 2)."""
+        mel = np.ascontiguousarray(mel, np.float32)
+        if mel.ndim != 2:
+            raise ShapeMismatchError(f"model: encoder: mel must be [{self.n_mels}, T], got {list(mel.shape)}")
+        nm, t = mel.shape
+        cap = (min(t, 2 * self.n_ctx) + 1) // 2
+        out = np.empty((max(cap, 1), self.n_state), np.float32)
+        rows = C.c_int32(0)
+        cptr = C.cast(C.byref(cancel), C.c_void_p) if cancel is not None else None
+        rc = lib().wh_encode(self._h, mel.ctypes.data, nm, t, out.ctypes.data, out.shape[0], C.byref(rows), cptr)
+        if rc != native.WH_OK:
+            _raise(rc)
+        return out[:rows.value]
+
+
 class HIPDecoder:
     """A decoder whose weights live in HBM (model.Decoder implementation)."""
 

@@ -32,6 +32,11 @@ class WhMeta(C.Structure):
                 ("n_state", C.c_uint32), ("n_vocab", C.c_uint32)]
 
 
+class WhEncMeta(C.Structure):
+    _fields_ = [("n_head", C.c_uint32), ("n_layer", C.c_uint32), ("n_ctx", C.c_uint32),
+                ("n_state", C.c_uint32), ("n_mels", C.c_uint32)]
+
+
 class WhDecodeParams(C.Structure):
     _fields_ = [("prompt", C.POINTER(C.c_int32)), ("prompt_len", C.c_int32), ("beam_size", C.c_int32),
                 ("temperature", C.c_float), ("logprob_thold", C.c_float), ("no_speech_thold", C.c_float),
@@ -74,6 +79,11 @@ _SIGS = [
     ("wh_gemv", C.c_int, [_P, _P, C.c_int32, _P, _P]),
     ("wh_model_create", C.c_int, [C.POINTER(WhTensor), C.c_int32, C.POINTER(WhMeta), C.c_int32, C.POINTER(_P)]),
     ("wh_model_load_gguf", C.c_int, [C.c_char_p, C.c_int32, C.POINTER(_P)]),
+    ("wh_encoder_create", C.c_int, [C.POINTER(WhTensor), C.c_int32, C.POINTER(WhEncMeta), C.c_int32, C.POINTER(_P)]),
+    ("wh_encoder_load_gguf", C.c_int, [C.c_char_p, C.c_int32, C.POINTER(_P)]),
+    ("wh_encoder_destroy", C.c_int, [_P]),
+    ("wh_encoder_hparams", C.c_int, [_P, C.POINTER(C.c_int32)]),
+    ("wh_encode", C.c_int, [_P, _P, C.c_int32, C.c_int32, _P, C.c_int32, C.POINTER(C.c_int32), _P]),
     ("wh_model_destroy", C.c_int, [_P]),
     ("wh_model_hparams", C.c_int, [_P, C.POINTER(C.c_int32)]),
     ("wh_model_set_eot", C.c_int, [_P, C.c_int32]),
