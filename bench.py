@@ -17,7 +17,8 @@ Also reported:
   bounded sample of the same workload.
 
 `--workload beam5|streams16` instead times one of the batched workloads (beam 5
-over the small decoder in Q5_1; 16 large-v3 Q4_1 streams) as one Decode call.
+over the small decoder in Q5_1; 16 large-v3 Q4_1 streams) as one Decode call;
+`--workload encoder` times the encoder forward of one 30 s window.
 `--gemv` instead runs the standalone quantised-GEMV microbench (rows x cols at
 batch 1 and 5 for each format, rotating over >= 1 GiB of distinct copies;
 back-to-back launches replayed from a HIP graph, time per launch).
@@ -290,6 +291,81 @@ def run_batched(args):
     print(json.dumps(out), flush=True)
 
 
+def encoder_flops(n_mels, d, n_layer, T):
+    """Multiply-add FLOPs (2 per MAC) of one encode of T mel frames: conv1
+    (3 n_mels -> d per frame), conv2 (3 d -> d per output frame, stride 2), and
+    per block the q, k, v, o projections (4 d^2), the MLP (8 d^2) and attention
+    (scores and weights . V, 2 T'^2 d) over T' = (T + 1) / 2 frames."""
+    tp = (T + 1) // 2
+    conv = 2 * T * d * 3 * n_mels + 2 * tp * d * 3 * d
+    block = 2 * tp * 12 * d * d + 2 * 2 * tp * tp * d
+    return conv + n_layer * block
+
+
+def run_encoder(args):
+    """The encoder forward (internal/model/encoder.go:265-338) of one 30 s window,
+    3000 mel frames -> 1500 rows, on the large-v3 encoder with seeded weights
+    quantised with the cmd/quantize rule. A step is one encode with the mel and
+    the output resident in HBM (wh_encode_device); the host-buffer call
+    (wh_encode, PCIe copies included) is timed beside it."""
+    wh = __graft_entry__.load_package()
+    if wh.native.device_count() < 1:
+        raise SystemExit("bench: no GPU visible")
+    config, qname = args.config, args.qtype
+    M, d, H, L, ctx = wh.synth.ENC_CONFIGS[config]
+    T = 2 * ctx
+    tensors, meta = wh.synth.make_encoder(config, QNAMES[qname])
+    mel = wh.synth.mel_input(config, M, T=T)
+    enc = wh.HIPEncoder(tensors, meta, device=0)
+    dmel, dout = wh.native.DevBuf.from_array(mel), wh.native.DevBuf(ctx * d * 4)
+    steps, warm = args.encoder_steps, 2
+    for _ in range(warm):
+        enc.encode_device(dmel.ptr.value, M, T, dout.ptr.value, ctx)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        enc.encode_device(dmel.ptr.value, M, T, dout.ptr.value, ctx)
+    dt = (time.perf_counter() - t0) / steps
+    got = dout.download((ctx, d), np.float32)
+    t1 = time.perf_counter()
+    host = enc.encode(mel)
+    dt_host = time.perf_counter() - t1
+    flops = encoder_flops(M, d, L, T)
+    tflops = flops / dt / 1e12
+    peak = 157.3
+    out = {"metric": f"encoder windows/s ({config} {qname}, 30 s window)", "value": round(1.0 / dt, 3),
+           "unit": "windows/s", "n_gpus": 1, "steps": steps, "warmup": warm, "ms_per_step": round(dt * 1e3, 3),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+           "data": "synthetic",
+           "config": {"workload": f"whisper {config} encoder, {qname} weights, {M}x{T} synthetic log-mel "
+                                  f"-> {ctx}x{d}, mel and output in HBM", "global_batch": 1},
+           "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
+                        "frac": round(tflops / peak, 4), "traffic": None,
+                        "scope": "whole encode (every kernel of the forward): algorithmic FLOPs / step time"},
+           "flops_per_step": flops,
+           "host_buffers_ms": round(dt_host * 1e3, 3),
+           "device_equals_host_path": bool(np.array_equal(got, host))}
+    dmel.free()
+    dout.free()
+    enc.close()
+    if args.cpu_tokens > 0:
+        from oracle import oracle as orc  # the checker, timed as the CPU baseline
+
+        threads = min(16, host_cores())
+        n_blk = 1
+        sub, smeta = wh.synth.make_encoder(config, QNAMES[qname], dims=(M, d, H, n_blk, ctx))
+        ref = orc.OracleEncoder(sub, smeta, threads=threads)
+        t2 = time.perf_counter()
+        ref.encode(mel)
+        dt_cpu = (time.perf_counter() - t2) * flops / encoder_flops(M, d, n_blk, T)
+        out["cpu_baseline"] = {"value": round(1.0 / dt_cpu, 5), "unit": "windows/s", "cores": threads,
+                               "kind": "port",
+                               "label": "restatement, not Go: the C oracle restating the Go encoder",
+                               "cpu_model": cpu_model(), "host_cores": host_cores(),
+                               "sample": f"conv stem + {n_blk} of {L} blocks over the full {T} frames, "
+                                         f"timed and scaled to the whole encoder by FLOPs"}
+    print(json.dumps(out), flush=True)
+
+
 class HipGraphs:
     """Stream capture into a HIP graph through the HIP runtime the library
     already loaded (the microbench's launch loop, replayed without Python)."""
@@ -424,8 +500,10 @@ def main():
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="first copy this many MiB device to device (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--gemv", action="store_true", help="run the standalone GEMV microbench instead")
-    ap.add_argument("--workload", choices=["beam5", "streams16"], default=None,
-                    help="run one of the batched workloads instead (beam 5 small Q5_1; 16 large-v3 Q4_1 streams)")
+    ap.add_argument("--workload", choices=["beam5", "streams16", "encoder"], default=None,
+                    help="run another workload instead: beam 5 small Q5_1; 16 large-v3 Q4_1 streams; the "
+                         "encoder forward of --config in --qtype")
+    ap.add_argument("--encoder-steps", type=int, default=10, help="timed encodes of the encoder workload")
     ap.add_argument("--gemv-formats", default="Q8_0,Q4_0,Q4_1,Q5_0,Q5_1")
     ap.add_argument("--gemv-single", action="store_true",
                     help="GEMV microbench: single launches between event pairs only, no graph "
@@ -437,6 +515,8 @@ def main():
         sys.exit(2)
     if args.gemv:
         run_gemv(args)
+    elif args.workload == "encoder":
+        run_encoder(args)
     elif args.workload:
         run_batched(args)
     else:

@@ -182,6 +182,13 @@ int wh_encoder_hparams(const wh_encoder *e, int32_t *out5);
  * between blocks (WH_ERR_CANCELLED). */
 int wh_encode(const wh_encoder *e, const float *mel, int32_t n_mels, int32_t T, float *out, int32_t out_cap,
               int32_t *out_rows, const volatile int32_t *cancel);
+/* The same with mel and out in device memory of the encoder's device (the
+ * encoder output then feeds a decoder without a host round trip). The call is
+ * synchronous: mel must be written before it is made, out is written when it
+ * returns. Calls on one handle run one at a time. No counterpart in the
+ * reference (its tensors live in host memory). */
+int wh_encode_device(const wh_encoder *e, const float *mel, int32_t n_mels, int32_t T, float *out,
+                     int32_t out_cap, int32_t *out_rows, const volatile int32_t *cancel);
 
 /* ---- Decode: the model.Decoder interface (internal/model/interfaces.go:22-25) */
 /* Mirrors model.DecoderParams (internal/model/interfaces.go:76-90); the

@@ -98,6 +98,30 @@ def test_encoder_frame_rules(wh, orc, gpu):
     enc.close()
 
 
+def test_encode_device_matches_host(wh, gpu):
+    """wh_encode_device (mel and output in device memory) gives the bits of
+    wh_encode: a full window, then a shorter one on the same handle (the
+    workspace is reused), then the 2 n_ctx + 1 frame rule read in place."""
+    dims = (16, 128, 2, 2, 40)
+    tensors, meta = wh.synth.make_encoder("edev", 8, dims=dims)
+    enc = wh.HIPEncoder(tensors, meta)
+    out = wh.native.DevBuf(40 * 128 * 4)
+    for T in (80, 37, 81):
+        print(f"encode_device T={T}", flush=True)
+        mel = wh.synth.mel_input("edev", 16, T=T)
+        want = enc.encode(mel)
+        dmel = wh.native.DevBuf.from_array(mel)
+        rows = enc.encode_device(dmel.ptr.value, 16, T, out.ptr.value, 40)
+        assert rows == want.shape[0] == min((T + 1) // 2, 40)
+        got = out.download((40, 128), np.float32)[:rows]
+        assert np.array_equal(got, want), T
+        dmel.free()
+    with pytest.raises(wh.native.WhError, match="output capacity"):
+        enc.encode_device(out.ptr.value, 16, 80, out.ptr.value, 39)
+    out.free()
+    enc.close()
+
+
 def test_encoder_cancelled(wh, gpu):
     """encoder_test.go:95-110: a cancelled context stops Encode with a
     cancellation error."""

@@ -29,6 +29,8 @@ void encoder_free(wh_encoder *e);
 int encoder_hparams(const wh_encoder *e, int32_t *o);
 int encode(const wh_encoder *e, const float *mel, int32_t n_mels, int32_t T, float *out, int32_t out_cap,
            int32_t *out_rows, const volatile int32_t *cancel);
+int encode_device(const wh_encoder *e, const float *mel, int32_t n_mels, int32_t T, float *out, int32_t out_cap,
+                  int32_t *out_rows, const volatile int32_t *cancel);
 int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t enc_len, int32_t enc_dim, int32_t shared,
                wh_seq **out);
 int seq_set_tokens(wh_seq *s, int32_t i, const int32_t *tokens, int32_t n, int32_t reset_kv);
@@ -379,6 +381,10 @@ int wh_encoder_hparams(const wh_encoder *e, int32_t *out5) { return encoder_hpar
 int wh_encode(const wh_encoder *e, const float *mel, int32_t n_mels, int32_t T, float *out, int32_t out_cap,
               int32_t *out_rows, const volatile int32_t *cancel) {
     return encode(e, mel, n_mels, T, out, out_cap, out_rows, cancel);
+}
+int wh_encode_device(const wh_encoder *e, const float *mel, int32_t n_mels, int32_t T, float *out, int32_t out_cap,
+                     int32_t *out_rows, const volatile int32_t *cancel) {
+    return encode_device(e, mel, n_mels, T, out, out_cap, out_rows, cancel);
 }
 int wh_model_destroy(wh_model *m) {
     model_free(m);

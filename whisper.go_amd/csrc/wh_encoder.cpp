@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -25,6 +26,11 @@ struct wh_encoder {
     };
     std::vector<Block> blocks;
     void *vec_alloc = nullptr;
+    // the forward's stream and workspace (sized for T = 2 n_ctx on first use),
+    // held for the encoder's lifetime; one encode at a time per handle
+    mutable hipStream_t st = nullptr;
+    mutable float *ws = nullptr;
+    mutable std::mutex mu;
 };
 
 namespace wh {
@@ -38,6 +44,8 @@ void encoder_free(wh_encoder *e) {
         for (DevMat *m : ms) devmat_free(*m);
     }
     if (e->vec_alloc) (void)hipFree(e->vec_alloc);
+    if (e->ws) (void)hipFree(e->ws);
+    if (e->st) (void)hipStreamDestroy(e->st);
     delete e;
 }
 
@@ -204,72 +212,131 @@ int encoder_hparams(const wh_encoder *e, int32_t *o) {
     return WH_OK;
 }
 
-// encoder.go:265-338 Encode.
-int encode(const wh_encoder *e, const float *mel, int32_t n_mels, int32_t T, float *out, int32_t out_cap,
-           int32_t *out_rows, const volatile int32_t *cancel) {
-    if (!e || !mel || !out || !out_rows) return fail(WH_ERR_INVALID, "model: encoder: null argument");
-    *out_rows = 0;
+namespace {
+
+// Frame-count rules of Encode (encoder.go:271-282): T = 2 n_ctx + 1 keeps the
+// first n_mels * 2 n_ctx values of the buffer (the same base, row stride 2 n_ctx);
+// T > 2 n_ctx is an error. Returns the frames the conv stem reads.
+int frames(const wh_encoder *e, int32_t n_mels, int32_t T, int32_t out_cap, int *tout) {
     if (n_mels != e->n_mels || T <= 0)
         return fail(WH_ERR_INVALID, "model: encoder: mel must be [" + std::to_string(e->n_mels) + ", T], got [" +
                                       std::to_string(n_mels) + " " + std::to_string(T) + "]");
-    // one extra STFT frame: the first n_mels * 2 n_ctx values of the buffer
     if (T == 2 * e->n_ctx + 1) T = 2 * e->n_ctx;
     if (T > 2 * e->n_ctx)
         return fail(WH_ERR_INVALID, "model: encoder: T=" + std::to_string(T) + " > 2*n_audio_ctx=" +
                                         std::to_string(2 * e->n_ctx));
-    const int d = e->n_state, H = e->n_head, tp = (T - 1) / 2 + 1;
-    if (out_cap < tp) return fail(WH_ERR_INVALID, "model: encoder: output capacity too small");
-    WH_HIP(hipSetDevice(e->device));
-    hipStream_t st;
-    WH_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
-    struct StreamGuard { hipStream_t s; ~StreamGuard() { (void)hipStreamDestroy(s); } } sg{st};
-    // workspace: mel, conv1 staging and output, conv2 staging, x, ln, q, k, v, attn, h
-    const size_t n_mel = (size_t)e->n_mels * T, n_e1 = (size_t)T * e->k1, n_c1 = (size_t)T * d;
-    const size_t n_e2 = (size_t)tp * 3 * d, n_x = (size_t)tp * d, n_h = (size_t)tp * 4 * d;
-    const size_t total = n_mel + n_e1 + n_c1 + n_e2 + 6 * n_x + n_h + 16 * 64;
-    float *ws = nullptr;
-    WH_HIP(hipMalloc(&ws, total * sizeof(float)));
-    struct FreeGuard { float *p; ~FreeGuard() { (void)hipFree(p); } } fg{ws};
+    if (out_cap < (T - 1) / 2 + 1) return fail(WH_ERR_INVALID, "model: encoder: output capacity too small");
+    *tout = T;
+    return WH_OK;
+}
+
+// Workspace of one forward at the largest frame count: mel staging, conv1
+// staging and output, conv2 staging, x, ln, q, k, v, attn, h.
+struct Work {
+    float *dmel, *e1, *c1, *e2, *x, *xln, *q, *k, *v, *att, *h;
+};
+size_t carve(const wh_encoder *e, float *base, Work *w) {
+    const int T = 2 * e->n_ctx, tp = e->n_ctx, d = e->n_state;
     size_t off = 0;
-    auto take = [&](size_t n) { float *p = ws + off; off += (n + 63) / 64 * 64; return p; };
-    float *dmel = take(n_mel), *e1 = take(n_e1), *c1 = take(n_c1), *e2 = take(n_e2), *x = take(n_x);
-    float *xln = take(n_x), *q = take(n_x), *k = take(n_x), *v = take(n_x), *att = take(n_x), *h = take(n_h);
-    // an already cancelled call stops where the reference's conv1 checks its context
-    if (cancel && *cancel) return fail(WH_ERR_CANCELLED, "model: encoder: conv1: ml: conv1d: context canceled");
-    WH_HIP(hipMemcpyAsync(dmel, mel, n_mel * sizeof(float), hipMemcpyHostToDevice, st));
+    auto take = [&](size_t n) { float *p = base ? base + off : nullptr; off += (n + 63) / 64 * 64; return p; };
+    w->dmel = take((size_t)e->n_mels * T);
+    w->e1 = take((size_t)T * e->k1);
+    w->c1 = take((size_t)T * d);
+    w->e2 = take((size_t)tp * 3 * d);
+    float **xs[] = {&w->x, &w->xln, &w->q, &w->k, &w->v, &w->att};
+    for (float **p : xs) *p = take((size_t)tp * d);
+    w->h = take((size_t)tp * 4 * d);
+    return off;
+}
+
+// The forward (encoder.go:284-338) of mel (device, [n_mels, T] rows T apart) into
+// out (device, [T', d]) on the encoder's stream; returns once out is written.
+int forward(const wh_encoder *e, const Work &w, const float *mel, int T, float *out, const volatile int32_t *cancel) {
+    const int d = e->n_state, H = e->n_head, tp = (T - 1) / 2 + 1;
+    const hipStream_t st = e->st;
     int rc;
     // conv stem (encoder.go:284-303): conv1 (stride 1) + GELU, conv2 (stride 2) + GELU,
     // frames first, plus the positional embedding of the first T' rows
-    if ((rc = launch_im2col(dmel, T, 1, e->n_mels, T, 1, T, e->k1, e1, st))) return rc;
-    if ((rc = launch_cross_gemm(e->conv1, e1, T, e->conv1b, c1, st))) return rc;
-    if ((rc = launch_gelu_add(c1, nullptr, (int64_t)n_c1, st))) return rc;
-    if ((rc = launch_im2col(c1, 1, d, d, T, 2, tp, 3 * d, e2, st))) return rc;
-    if ((rc = launch_cross_gemm(e->conv2, e2, tp, e->conv2b, x, st))) return rc;
-    if ((rc = launch_gelu_add(x, e->pos, (int64_t)n_x, st))) return rc;
+    if ((rc = launch_im2col(mel, T, 1, e->n_mels, T, 1, T, e->k1, w.e1, st))) return rc;
+    if ((rc = launch_cross_gemm(e->conv1, w.e1, T, e->conv1b, w.c1, st))) return rc;
+    if ((rc = launch_gelu_add(w.c1, nullptr, (int64_t)T * d, st))) return rc;
+    if ((rc = launch_im2col(w.c1, 1, d, d, T, 2, tp, 3 * d, w.e2, st))) return rc;
+    if ((rc = launch_cross_gemm(e->conv2, w.e2, tp, e->conv2b, w.x, st))) return rc;
+    if ((rc = launch_gelu_add(w.x, e->pos, (int64_t)tp * d, st))) return rc;
     for (int i = 0; i < e->n_layer; i++) {
         const wh_encoder::Block &b = e->blocks[i];
         // self-attention sub-layer (encoder.go:310-317, 340-379)
-        if ((rc = launch_layernorm(x, b.ln1w, b.ln1b, xln, tp, d, st))) return rc;
-        if ((rc = launch_cross_gemm(b.q, xln, tp, b.qb, q, st))) return rc;
-        if ((rc = launch_cross_gemm(b.k, xln, tp, nullptr, k, st))) return rc;
-        if ((rc = launch_cross_gemm(b.v, xln, tp, b.vb, v, st))) return rc;
-        if ((rc = launch_enc_attn(q, k, v, tp, d, H, att, st))) return rc;
-        if ((rc = launch_cross_gemm(b.o, att, tp, b.ob, x, st, 0, x))) return rc;
+        if ((rc = launch_layernorm(w.x, b.ln1w, b.ln1b, w.xln, tp, d, st))) return rc;
+        if ((rc = launch_cross_gemm(b.q, w.xln, tp, b.qb, w.q, st))) return rc;
+        if ((rc = launch_cross_gemm(b.k, w.xln, tp, nullptr, w.k, st))) return rc;
+        if ((rc = launch_cross_gemm(b.v, w.xln, tp, b.vb, w.v, st))) return rc;
+        if ((rc = launch_enc_attn(w.q, w.k, w.v, tp, d, H, w.att, st))) return rc;
+        if ((rc = launch_cross_gemm(b.o, w.att, tp, b.ob, w.x, st, 0, w.x))) return rc;
         // MLP sub-layer (encoder.go:319-325, 383-396)
-        if ((rc = launch_layernorm(x, b.ln2w, b.ln2b, xln, tp, d, st))) return rc;
-        if ((rc = launch_cross_gemm(b.fc1, xln, tp, b.fc1b, h, st, 1))) return rc;
-        if ((rc = launch_cross_gemm(b.fc2, h, tp, b.fc2b, x, st, 0, x))) return rc;
-        // one block at a time in flight, so a cancellation is seen within a block
-        // (encoder.go:327-329 checks after every block)
-        WH_HIP(hipStreamSynchronize(st));
-        if (cancel && *cancel)
-            return fail(WH_ERR_CANCELLED,
-                        "model: encoder: cancelled after block " + std::to_string(i) + ": context canceled");
+        if ((rc = launch_layernorm(w.x, b.ln2w, b.ln2b, w.xln, tp, d, st))) return rc;
+        if ((rc = launch_cross_gemm(b.fc1, w.xln, tp, b.fc1b, w.h, st, 1))) return rc;
+        if ((rc = launch_cross_gemm(b.fc2, w.h, tp, b.fc2b, w.x, st, 0, w.x))) return rc;
+        // encoder.go:327-329 checks the context after every block: with a flag
+        // to poll, one block at a time is in flight
+        if (cancel) {
+            WH_HIP(hipStreamSynchronize(st));
+            if (*cancel)
+                return fail(WH_ERR_CANCELLED,
+                            "model: encoder: cancelled after block " + std::to_string(i) + ": context canceled");
+        }
     }
-    if ((rc = launch_layernorm(x, e->lnw, e->lnb, xln, tp, d, st))) return rc;
-    WH_HIP(hipMemcpyAsync(out, xln, n_x * sizeof(float), hipMemcpyDeviceToHost, st));
+    if ((rc = launch_layernorm(w.x, e->lnw, e->lnb, out, tp, d, st))) return rc;
     WH_HIP(hipStreamSynchronize(st));
+    return WH_OK;
+}
+
+// The stream and the workspace, made on the first encode of the handle.
+int prepare(const wh_encoder *e, Work *w) {
+    WH_HIP(hipSetDevice(e->device));
+    if (!e->st) WH_HIP(hipStreamCreateWithFlags(&e->st, hipStreamNonBlocking));
+    if (!e->ws) WH_HIP(hipMalloc(&e->ws, carve(e, nullptr, w) * sizeof(float)));
+    carve(e, e->ws, w);
+    return WH_OK;
+}
+
+}  // namespace
+
+// encoder.go:265-338 Encode: host mel in, host output out.
+int encode(const wh_encoder *e, const float *mel, int32_t n_mels, int32_t T, float *out, int32_t out_cap,
+           int32_t *out_rows, const volatile int32_t *cancel) {
+    if (!e || !mel || !out || !out_rows) return fail(WH_ERR_INVALID, "model: encoder: null argument");
+    *out_rows = 0;
+    int rc, Tr;
+    if ((rc = frames(e, n_mels, T, out_cap, &Tr))) return rc;
+    // an already cancelled call stops where the reference's conv1 checks its context
+    if (cancel && *cancel) return fail(WH_ERR_CANCELLED, "model: encoder: conv1: ml: conv1d: context canceled");
+    std::lock_guard<std::mutex> lk(e->mu);
+    Work w;
+    if ((rc = prepare(e, &w))) return rc;
+    const int tp = (Tr - 1) / 2 + 1;
+    WH_HIP(hipMemcpyAsync(w.dmel, mel, sizeof(float) * e->n_mels * Tr, hipMemcpyHostToDevice, e->st));
+    if ((rc = forward(e, w, w.dmel, Tr, w.xln, cancel))) return rc;
+    WH_HIP(hipMemcpyAsync(out, w.xln, sizeof(float) * tp * e->n_state, hipMemcpyDeviceToHost, e->st));
+    WH_HIP(hipStreamSynchronize(e->st));
     *out_rows = tp;
+    return WH_OK;
+}
+
+// The same with mel and the output in device memory of the encoder's device.
+int encode_device(const wh_encoder *e, const float *mel, int32_t n_mels, int32_t T, float *out, int32_t out_cap,
+                  int32_t *out_rows, const volatile int32_t *cancel) {
+    if (!e || !mel || !out || !out_rows) return fail(WH_ERR_INVALID, "model: encoder: null argument");
+    *out_rows = 0;
+    int rc, Tr;
+    if ((rc = frames(e, n_mels, T, out_cap, &Tr))) return rc;
+    if (cancel && *cancel) return fail(WH_ERR_CANCELLED, "model: encoder: conv1: ml: conv1d: context canceled");
+    std::lock_guard<std::mutex> lk(e->mu);
+    Work w;
+    if ((rc = prepare(e, &w))) return rc;
+    // mel rows stay T apart in the caller's buffer, except for the 2 n_ctx + 1
+    // case, whose first n_mels * 2 n_ctx values are read as [n_mels, 2 n_ctx]
+    if ((rc = forward(e, w, mel, Tr, out, cancel))) return rc;
+    *out_rows = (Tr - 1) / 2 + 1;
     return WH_OK;
 }
 

@@ -165,6 +165,16 @@ class HIPEncoder:
             _raise(rc)
         return out[:rows.value]
 
+    def encode_device(self, mel_ptr, n_mels, T, out_ptr, out_cap, cancel: Optional[C.c_int32] = None):
+        """Encode with mel ([n_mels, T] float32) and the output ([out_cap, n_state]
+        float32) in device memory, given as addresses; returns the output rows."""
+        rows = C.c_int32(0)
+        cptr = C.cast(C.byref(cancel), C.c_void_p) if cancel is not None else None
+        rc = lib().wh_encode_device(self._h, int(mel_ptr), n_mels, T, int(out_ptr), out_cap, C.byref(rows), cptr)
+        if rc != native.WH_OK:
+            _raise(rc)
+        return rows.value
+
 
 class HIPDecoder:
     """A decoder whose weights live in HBM (model.Decoder implementation)."""

@@ -84,6 +84,7 @@ _SIGS = [
     ("wh_encoder_destroy", C.c_int, [_P]),
     ("wh_encoder_hparams", C.c_int, [_P, C.POINTER(C.c_int32)]),
     ("wh_encode", C.c_int, [_P, _P, C.c_int32, C.c_int32, _P, C.c_int32, C.POINTER(C.c_int32), _P]),
+    ("wh_encode_device", C.c_int, [_P, _P, C.c_int32, C.c_int32, _P, C.c_int32, C.POINTER(C.c_int32), _P]),
     ("wh_model_destroy", C.c_int, [_P]),
     ("wh_model_hparams", C.c_int, [_P, C.POINTER(C.c_int32)]),
     ("wh_model_set_eot", C.c_int, [_P, C.c_int32]),
