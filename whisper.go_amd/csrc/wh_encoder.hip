@@ -37,141 +37,158 @@ __global__ void k_gelu_add(float *x, const float *pos, int64_t n) {
     }
 }
 
-// DPP exchange within rows of 16 lanes
-template <int CTRL>
-__device__ __forceinline__ float dpp16(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-// max and sum over the 16 lanes of a row, left in every lane
-__device__ __forceinline__ float row16_max(float v) {
-    v = fmaxf(v, dpp16<0xB1>(v));
-    v = fmaxf(v, dpp16<0x4E>(v));
-    v = fmaxf(v, dpp16<0x141>(v));
-    return fmaxf(v, dpp16<0x140>(v));
-}
-__device__ __forceinline__ float row16_sum(float v) {
-    v += dpp16<0xB1>(v);
-    v += dpp16<0x4E>(v);
-    v += dpp16<0x141>(v);
-    return v + dpp16<0x140>(v);
-}
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int ATQ = 64;         // queries per workgroup
-constexpr int ATK = 64;         // keys per tile
-constexpr int ATS = ATQ + 4;    // LDS row stride (floats): 16-byte rows, rotated banks
-constexpr size_t AT_LDS = 4 * 64 * ATS * sizeof(float);
+constexpr int AK = 64;       // keys per tile
+constexpr int AKS = AK + 4;  // K tile row stride (floats): 16-byte rows, 16 rows cover the 64 banks once
 
-// SDPA of one head, 64 queries per workgroup, head size 64
+// SDPA of one head with head size 64 on the fp32 matrix cores
 // (ml/attention.go:193-281 with the fast-exp softmax of attention.go:93-131):
 // scores = (q . k) * scale; weight = fastexp(score - row max) / row sum;
-// out = weights . V. Pass 1 finds every row's maximum over all keys; pass 2
-// recomputes the scores tile by tile, forms the fast-exp weights against that
-// maximum and accumulates weights . V and the row sums; the output is the
-// accumulation times 1 / sum. Thread (qi, ki) holds queries 4qi..4qi+3 against
-// keys (pass 1, scores) or output columns (pass 2, P.V) 4ki..4ki+3; the 16
-// threads of a query group are one DPP row. Q, K, V, out are [T, d] with head
-// h in columns 64h..64h+63.
-__global__ __launch_bounds__(256) void k_enc_attn64(const float *Q, const float *K, const float *V, int T, int d,
-                                                     float scale, float *out) {
-    extern __shared__ float lds[];
-    float(*Qt)[ATS] = (float(*)[ATS])lds;                  // [dim][query]
-    float(*Kt)[ATS] = (float(*)[ATS])(lds + 64 * ATS);     // [dim][key]
-    float(*Vs)[ATS] = (float(*)[ATS])(lds + 128 * ATS);    // [key][dim]
-    float(*Pt)[ATS] = (float(*)[ATS])(lds + 192 * ATS);    // [key][query]
-    const int h = blockIdx.y, q0 = blockIdx.x * ATQ, tid = threadIdx.x;
-    const int qi = tid >> 4, ki = tid & 15;
+// out = weights . V. Each wave owns 32 queries; the QW waves of a workgroup
+// share the K and V tiles of 64 keys staged in LDS (the next tile's loads in
+// flight while the current one is used).
+//
+// The products are formed transposed, S^T = K Q^T and O^T = V^T P^T, with
+// v_mfma_f32_32x32x2f32: its accumulator gives lane l the column l % 32 (one
+// query) and rows 8 (i / 4) + 4 (l / 32) + i % 4 in register i (keys, or output
+// dimensions). A query's row maximum and sum are then a lane's own values and
+// its partner lane l ^ 32, and register i of the weights is exactly the B
+// operand (key 8 (i / 4) + i % 4 from lanes 0-31, that key + 4 from lanes
+// 32-63) of the P.V step that takes the V rows of those two keys as A.
+// In S^T = K Q^T, MFMA k-index 0 carries dimensions 0-31 and index 1
+// dimensions 32-63, so each lane keeps its query's half row of q in registers.
+//
+// Pass 1 finds every row's maximum of scale * score over all keys; pass 2
+// recomputes the scores, forms the fast-exp weights against that maximum,
+// accumulates weights . V and the row sums; the output is the accumulation times
+// 1 / sum. Keys past T weigh 0 (their V rows are staged as zeros), queries past T
+// are not stored. Q, K, V, out are [T, d] with head h in columns 64h..64h+63.
+template <int QW>
+__global__ __launch_bounds__(64 * QW) void k_enc_attn_mfma(const float *Q, const float *K, const float *V, int T,
+                                                           int d, float scale, float *out) {
+    constexpr int NT = 64 * QW, NL = AK * 16 / NT;  // float4 of a tile per thread
+    static_assert(AK * 16 % NT == 0, "a tile is whole float4 rounds of the workgroup");
+    __shared__ float Ks[AK][AKS];
+    __shared__ float Vs[AK][64];
+    const int h = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int ql = lane & 31, half = lane >> 5;
+    const int q = blockIdx.x * 32 * QW + wave * 32 + ql;
     const size_t col = (size_t)h * 64;
-    for (int i = tid; i < 64 * 64; i += 256) {
-        const int t = i >> 6, c = i & 63;
-        Qt[c][t] = q0 + t < T ? Q[(size_t)(q0 + t) * d + col + c] : 0.0f;
+    float qr[32];
+    {
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 *src = (const float4 *)(Q + (size_t)q * d + col + 32 * half);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float4 v = q < T ? src[j] : z;
+            qr[4 * j] = v.x; qr[4 * j + 1] = v.y; qr[4 * j + 2] = v.z; qr[4 * j + 3] = v.w;
+        }
     }
-    // scores of the thread's 4 x 4 block against the staged key tile
-    const auto tile_scores = [&](float (&s)[4][4]) __attribute__((always_inline)) {
+    // tile staging: float4 i of a tile is key i / 16, dimensions 4 (i % 16) ..
+    const auto load_tile = [&](const float *src, int k0, float4 (&r)[NL]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) s[i][j] = 0.0f;
-#pragma unroll 8
-        for (int c = 0; c < 64; c++) {
-            const float4 qv = *(const float4 *)&Qt[c][4 * qi];
-            const float4 kv = *(const float4 *)&Kt[c][4 * ki];
-            const float qa[4] = {qv.x, qv.y, qv.z, qv.w}, ka[4] = {kv.x, kv.y, kv.z, kv.w};
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) s[i][j] = __builtin_fmaf(qa[i], ka[j], s[i][j]);
+        for (int j = 0; j < NL; j++) {
+            const int i = tid + j * NT, key = k0 + (i >> 4);
+            r[j] = key < T ? *(const float4 *)(src + (size_t)key * d + col + 4 * (i & 15))
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
-    const auto stage_k = [&](int k0) __attribute__((always_inline)) {
-        for (int i = tid; i < 64 * 64; i += 256) {
-            const int t = i >> 6, c = i & 63;
-            Kt[c][t] = k0 + t < T ? K[(size_t)(k0 + t) * d + col + c] : 0.0f;
+    const auto store_k = [&](const float4 (&r)[NL]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NL; j++) {
+            const int i = tid + j * NT;
+            *(float4 *)&Ks[i >> 4][4 * (i & 15)] = r[j];
         }
     };
+    const auto store_v = [&](const float4 (&r)[NL]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NL; j++) {
+            const int i = tid + j * NT;
+            *(float4 *)&Vs[i >> 4][4 * (i & 15)] = r[j];
+        }
+    };
+    // S^T of the staged tile: s0 keys 0-31, s1 keys 32-63, this lane's query
+    const auto scores = [&](f32x16 &s0, f32x16 &s1) __attribute__((always_inline)) {
+        s0 = f32x16{};
+        s1 = f32x16{};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float4 ka = *(const float4 *)&Ks[ql][32 * half + 4 * j];
+            const float4 kb = *(const float4 *)&Ks[32 + ql][32 * half + 4 * j];
+            s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.x, qr[4 * j], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kb.x, qr[4 * j], s1, 0, 0, 0);
+            s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.y, qr[4 * j + 1], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kb.y, qr[4 * j + 1], s1, 0, 0, 0);
+            s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.z, qr[4 * j + 2], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kb.z, qr[4 * j + 2], s1, 0, 0, 0);
+            s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.w, qr[4 * j + 3], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kb.w, qr[4 * j + 3], s1, 0, 0, 0);
+        }
+    };
+    // key of register i within its 32-key half of the tile
+    const auto rkey = [&](int i) __attribute__((always_inline)) { return 8 * (i >> 2) + 4 * half + (i & 3); };
+    float4 kr[NL], vr[NL];
     // pass 1: row maxima
-    float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-    for (int k0 = 0; k0 < T; k0 += ATK) {
+    float mx = -INFINITY;
+    load_tile(K, 0, kr);
+    for (int k0 = 0; k0 < T; k0 += AK) {
         __syncthreads();
-        stage_k(k0);
+        store_k(kr);
         __syncthreads();
-        float s[4][4];
-        tile_scores(s);
+        if (k0 + AK < T) load_tile(K, k0 + AK, kr);
+        f32x16 s0, s1;
+        scores(s0, s1);
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (k0 + 4 * ki + j < T)
-#pragma unroll
-                for (int i = 0; i < 4; i++) mx[i] = fmaxf(mx[i], s[i][j] * scale);
+        for (int i = 0; i < 16; i++) {
+            if (k0 + rkey(i) < T) mx = fmaxf(mx, s0[i] * scale);
+            if (k0 + 32 + rkey(i) < T) mx = fmaxf(mx, s1[i] * scale);
+        }
     }
-#pragma unroll
-    for (int i = 0; i < 4; i++) mx[i] = row16_max(mx[i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     // pass 2: fast-exp weights, P.V and row sums
-    float acc[4][4], rs[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = 0.0f;
-    for (int k0 = 0; k0 < T; k0 += ATK) {
+    f32x16 o0 = {}, o1 = {};  // output dimensions 0-31 and 32-63
+    float rs = 0.0f;
+    load_tile(K, 0, kr);
+    load_tile(V, 0, vr);
+    for (int k0 = 0; k0 < T; k0 += AK) {
         __syncthreads();
-        stage_k(k0);
-        for (int i = tid; i < 64 * 64; i += 256) {
-            const int t = i >> 6, c = i & 63;
-            Vs[t][c] = k0 + t < T ? V[(size_t)(k0 + t) * d + col + c] : 0.0f;
+        store_k(kr);
+        store_v(vr);
+        __syncthreads();
+        if (k0 + AK < T) {
+            load_tile(K, k0 + AK, kr);
+            load_tile(V, k0 + AK, vr);
         }
-        __syncthreads();
-        float s[4][4];
-        tile_scores(s);
+        f32x16 s0, s1;
+        scores(s0, s1);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const bool ok = k0 + 4 * ki + j < T;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float e = ok ? fast_exp(s[i][j] * scale - mx[i]) : 0.0f;
-                rs[i] += e;
-                Pt[4 * ki + j][4 * qi + i] = e;
-            }
+        for (int i = 0; i < 16; i++) {
+            s0[i] = k0 + rkey(i) < T ? fast_exp(s0[i] * scale - mx) : 0.0f;
+            s1[i] = k0 + 32 + rkey(i) < T ? fast_exp(s1[i] * scale - mx) : 0.0f;
+            rs += s0[i] + s1[i];
         }
-        __syncthreads();
-#pragma unroll 8
-        for (int k = 0; k < ATK; k++) {
-            const float4 pv = *(const float4 *)&Pt[k][4 * qi];
-            const float4 vv = *(const float4 *)&Vs[k][4 * ki];
-            const float pa[4] = {pv.x, pv.y, pv.z, pv.w}, va[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] = __builtin_fmaf(pa[i], va[j], acc[i][j]);
+        for (int i = 0; i < 16; i++) {
+            const float *va = Vs[rkey(i)], *vb = Vs[32 + rkey(i)];
+            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(va[ql], s0[i], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(va[32 + ql], s0[i], o1, 0, 0, 0);
+            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[ql], s1[i], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[32 + ql], s1[i], o1, 0, 0, 0);
         }
     }
+    rs += __shfl_xor(rs, 32, 64);
+    if (q >= T) return;
+    // the row maximum's own weight is fast_exp(0) = 1, so rs >= 1 (the
+    // reference's uniform-weight branch for a zero sum cannot be taken)
+    const float inv = 1.0f / rs;
+    float *dst = out + (size_t)q * d + col + 4 * half;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float sum = row16_sum(rs[i]);
-        const int t = q0 + 4 * qi + i;
-        if (t >= T) continue;
-        // the row maximum's own weight is fast_exp(0) = 1, so sum >= 1 (the
-        // reference's uniform-weight branch for sum == 0 cannot be taken)
-        const float inv = 1.0f / sum;
-        float4 o = make_float4(acc[i][0] * inv, acc[i][1] * inv, acc[i][2] * inv, acc[i][3] * inv);
-        *(float4 *)&out[(size_t)t * d + col + 4 * ki] = o;
+    for (int a = 0; a < 4; a++) {
+        *(float4 *)(dst + 8 * a) = make_float4(o0[4 * a] * inv, o0[4 * a + 1] * inv, o0[4 * a + 2] * inv,
+                                               o0[4 * a + 3] * inv);
+        *(float4 *)(dst + 32 + 8 * a) = make_float4(o1[4 * a] * inv, o1[4 * a + 1] * inv, o1[4 * a + 2] * inv,
+                                                    o1[4 * a + 3] * inv);
     }
 }
 
@@ -234,11 +251,11 @@ int launch_gelu_add(float *x, const float *pos, int64_t n, hipStream_t s) {
 int launch_enc_attn(const float *Q, const float *K, const float *V, int T, int d, int H, float *out, hipStream_t s) {
     const int hd = d / H;
     const float scale = (float)(1.0 / sqrt((double)hd));
-    if (hd == 64 && d % 4 == 0) {
-        WH_HIP(hipFuncSetAttribute((const void *)k_enc_attn64, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   (int)AT_LDS));
-        hipLaunchKernelGGL(k_enc_attn64, dim3((T + ATQ - 1) / ATQ, H), dim3(256), AT_LDS, s, Q, K, V, T, d, scale,
-                           out);
+    if (hd == 64 && d % 4 == 0 && ((uintptr_t)Q & 15) == 0 && ((uintptr_t)K & 15) == 0 &&
+        ((uintptr_t)V & 15) == 0 && ((uintptr_t)out & 15) == 0) {
+        constexpr int QW = 4;
+        hipLaunchKernelGGL(k_enc_attn_mfma<QW>, dim3((T + 32 * QW - 1) / (32 * QW), H), dim3(64 * QW), 0, s, Q, K, V,
+                           T, d, scale, out);
     } else {
         hipLaunchKernelGGL(k_enc_attn_any, dim3(T, H), dim3(64), (size_t)T * sizeof(float), s, Q, K, V, T, d, hd,
                            scale, out);
