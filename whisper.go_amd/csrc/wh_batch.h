@@ -35,11 +35,13 @@ struct BArgs {
     MatView tok;                          // token embedding = tied logits matrix
     const float *pos_emb, *lnw, *lnb;
     const int32_t *tokv, *posv, *active;  // [S]
-    float *x, *x2, *q, *h, *logits;       // activations [S][d] ([S][4d] for h, [S][V] logits)
-    float *sa;                            // self-attention outputs [L][S][d]
-    float *pv, *psum;                     // per chunk of a head: P.V [S][H][xchunks][64], weight sums [S][H][xchunks]
-    uint64_t *xmax;                       // per chunk: {phase, maximum score} pairs [S][H][xchunks]
-    unsigned *flags;                      // [grid] barrier phases
+    // exchanged between workgroups as {tag, value} pairs (value in the low word):
+    // activations [S][d] ([S][4d] for h), self-attention outputs [L][S][d], and
+    // per key chunk of a head its P.V and weight sum [S][H][xchunks][65] and its
+    // maximum score [S][H][xchunks]
+    uint64_t *x, *x2, *q, *h, *attn, *sa, *pv, *xmax;
+    float *logits;                        // [S][V]
+    unsigned *flags;                      // [grid] last published phase
     unsigned *err;                        // set when a wait gives up
     float scale;                          // 1/sqrt(64)
 };

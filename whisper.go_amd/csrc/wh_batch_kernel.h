@@ -18,10 +18,10 @@
 //       one chunk per head and several heads per workgroup when S * H exceeds
 //       the grid);
 //       scores into LDS, the head maximum from the chunk maxima of the head's
-//       workgroups (a {phase, value} exchange among them, no grid barrier),
-//       fast-exp weights against it and the chunk's partial P.V
-//   F   cross out rows on attn = (sum of the head's partial P.V) / (sum of its
-//       weight sums), combined while staging: x2 = (x + sa_l) + (Wo_c.attn + b)
+//       workgroups, fast-exp weights against it and the chunk's partial P.V;
+//       the head's first chunk then forms attn = (sum of the chunks' P.V) /
+//       (sum of their weight sums)
+//   F   cross out rows: x2 = (x + sa_l) + (Wo_c.attn + b)
 //   G   LN3(x2); fc1 rows + GELU -> h
 //   H   fc2 rows: x = x2 + (W2.h + b2)
 // and the step ends with the final LN and the tied logits rows. When a state is
@@ -37,12 +37,17 @@
 // differs.
 //
 // Exchange between workgroups: every value another workgroup reads within the
-// launch is stored and loaded with relaxed agent-scope atomics, which bypass
-// the per-XCD caches, so the barrier needs no cache writeback or invalidation:
-// each wave waits for its stores to complete, the workgroup publishes its phase
-// number and waits until all workgroups have published it. Every wait is
-// bounded: on expiry the error word is set, later waits return at once, and the
-// host reports a failure.
+// launch travels as a {tag, value} pair, stored and loaded with one relaxed
+// agent-scope 64-bit atomic (past the per-XCD caches). The tag is the phase
+// that wrote it (a counter every workgroup advances alike, continued across
+// launches); a reader polls the pairs themselves until they carry the phase it
+// needs, so a phase waits only for the values it reads, with no grid barrier,
+// store-completion wait or separate flag. A buffer is rewritten only after every
+// reader of its previous value has published a later value that the writer
+// waited for. Only the KV rows at position 0, read by the next phase as plain
+// floats, are followed by a grid barrier. Every wait is bounded: on expiry the
+// error word is set, the values are taken as they are, and the host reports a
+// failure.
 #pragma once
 // Included by the per-format sources wh_batch_q*.hip, each of which
 // instantiates the kernel for one weight type (the instantiations compile in
@@ -61,6 +66,7 @@ namespace batch {
 constexpr int NWV = NT / 64;
 constexpr int XBLK = XBUDGET / 128;  // staged 32-float blocks, over all states
 constexpr unsigned SPIN_MAX = 1u << 22;
+constexpr int PU = 4, PU2 = 2;  // pair slots per thread loaded before a wait (one vector, two vectors)
 
 // ---- cross-lane sums ---------------------------------------------------------------
 // DPP lane exchange within rows of 16 lanes
@@ -142,9 +148,32 @@ __device__ __forceinline__ void stx(float *p, float v) {
 // this wave's stores (and loads) have completed
 __device__ __forceinline__ void stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// ---- {tag, value} pairs ------------------------------------------------------------
+__device__ __forceinline__ uint64_t ldp(const uint64_t *p) {
+    return __hip_atomic_load((gcu64 *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void stp(uint64_t *p, float v, unsigned t) {
+    __hip_atomic_store((gu64 *)p, ((uint64_t)t << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool ready(uint64_t v, unsigned t) { return (unsigned)(v >> 32) >= t; }
+__device__ __forceinline__ float val(uint64_t v) { return __uint_as_float((uint32_t)v); }
+
 // ---- grid barrier -------------------------------------------------------------------
 __device__ __forceinline__ bool failed(unsigned *err) {
     return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+}
+
+// The value of pair p, v as already loaded, once its tag reaches t.
+__device__ __forceinline__ float waitp(const uint64_t *p, uint64_t v, unsigned t, unsigned *err) {
+    for (unsigned spins = 0; !ready(v, t); spins++) {
+        if (spins > SPIN_MAX || failed(err)) {
+            atomicOr(err, 1u);
+            break;
+        }
+        v = ldp(p);
+    }
+    return val(v);
 }
 
 __device__ __forceinline__ void gbar(unsigned *flags, unsigned *err, unsigned &g) {
@@ -290,9 +319,77 @@ __device__ __forceinline__ void burst(int S, int cols, int c0, int nbc, Src src,
     }
 }
 
-template <class Src>
-__device__ __forceinline__ void stage_cols(int S, int cols, int c0, int nbc, Src src, float4 *xs, float *sx, bool sums) {
-    burst(S, cols, c0, nbc, src, xs);
+// The same from the pair vector a (plus b, element by element, when TWO), rows
+// ld pairs apart, once the pairs' tags reach ta (tb); rows of inactive states
+// stage as zeros and are not waited for. Each thread loads U slots (4 pairs each)
+// before it waits for any, then re-reads only the pending pairs.
+template <int U, bool TWO>
+__device__ __forceinline__ void burst_pairs(int S, unsigned amask, int cols, int c0, int nbc, const uint64_t *a,
+                                            unsigned ta, const uint64_t *b, unsigned tb, size_t ld, float4 *xs,
+                                            unsigned *err) {
+    const int n = S * nbc * 8;
+    for (int i0 = threadIdx.x; i0 < n; i0 += NT * U) {
+        uint64_t va[U][4], vb[U][TWO ? 4 : 1];
+        size_t off[U];
+        bool on[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = i0 + u * NT, s = i / (nbc * 8), r = i - s * (nbc * 8);
+            const int col = (c0 + (r >> 3)) * 32 + 4 * (r & 7);
+            on[u] = i < n && col < cols && ((amask >> s) & 1u);
+            off[u] = on[u] ? (size_t)s * ld + col : 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                va[u][k] = on[u] ? ldp(a + off[u] + k) : 0;
+                if constexpr (TWO) vb[u][k] = on[u] ? ldp(b + off[u] + k) : 0;
+            }
+        }
+        for (unsigned spins = 0;; spins++) {
+            bool ok = true;
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    ok = ok && (!on[u] || ready(va[u][k], ta));
+                    if constexpr (TWO) ok = ok && (!on[u] || ready(vb[u][k], tb));
+                }
+            if (ok) break;
+            if (spins > SPIN_MAX || failed(err)) {
+                atomicOr(err, 1u);
+                break;
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    if (on[u] && !ready(va[u][k], ta)) va[u][k] = ldp(a + off[u] + k);
+                    if constexpr (TWO)
+                        if (on[u] && !ready(vb[u][k], tb)) vb[u][k] = ldp(b + off[u] + k);
+                }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = i0 + u * NT;
+            if (i < n) {
+                const int s = i / (nbc * 8), r = i - s * (nbc * 8);
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (on[u]) {
+                    if constexpr (TWO)
+                        v = make_float4(val(va[u][0]) + val(vb[u][0]), val(va[u][1]) + val(vb[u][1]),
+                                        val(va[u][2]) + val(vb[u][2]), val(va[u][3]) + val(vb[u][3]));
+                    else
+                        v = make_float4(val(va[u][0]), val(va[u][1]), val(va[u][2]), val(va[u][3]));
+                }
+                xs[slot(s, nbc, r >> 3, r & 7)] = v;
+            }
+        }
+    }
+}
+
+// fill() stages the columns, then their block sums when asked.
+template <class Fill>
+__device__ __forceinline__ void stage_cols(int S, int nbc, Fill fill, float4 *xs, float *sx, bool sums) {
+    fill();
     __syncthreads();
     if (sums) {
         stage_sums(S, nbc, xs, sx);
@@ -300,18 +397,18 @@ __device__ __forceinline__ void stage_cols(int S, int cols, int c0, int nbc, Src
     }
 }
 
-// LayerNorm (internal/ml/ops.go:153-202) of the d-element rows src(s, .) of the
-// S states into the staged layout: the mean, then the mean of squared
+// LayerNorm (internal/ml/ops.go:153-202) of the d-element rows of the S states,
+// which fill() stages, in the staged layout: the mean, then the mean of squared
 // deviations, std = float32(sqrt(float64(var + eps))), w*(x-mean)/std + b. The
-// rows and the weights are loaded in one burst; the statistics take one wave per
-// state, the normalisation every thread.
-template <class Src>
-__device__ __forceinline__ void stage_ln(int S, int d, Src src, const float *w, const float *bb, const Lds &L, bool sums) {
+// weights are loaded before the rows; the statistics take one wave per state,
+// the normalisation every thread.
+template <class Fill>
+__device__ __forceinline__ void stage_ln(int S, int d, Fill fill, const float *w, const float *bb, const Lds &L, bool sums) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int nbc = d / 32, dq = d / 4;
     const int iw = min((int)threadIdx.x, dq - 1);  // d <= 4 NT
     const float4 wr = ldg4(w + 4 * iw), br = ldg4(bb + 4 * iw);
-    burst(S, d, 0, nbc, src, L.xs);
+    fill();
     if ((int)threadIdx.x < dq) {
         ((float4 *)L.lw)[threadIdx.x] = wr;
         ((float4 *)L.lb)[threadIdx.x] = br;
@@ -431,17 +528,17 @@ __device__ __forceinline__ void dot_blk(const Blk (&rb)[RW], int nr, int S, int 
 // The epilogue operand pre(s, row) of each of the lane's rows for the state the
 // lane finishes (lane % G), loaded before the dot products so that its latency
 // overlaps the weight loads.
-template <int G, class Pre>
-__device__ __forceinline__ void load_pre(int P, int row1, int S, Pre pre, float2 (&ad)[RW]) {
+template <int G, class Pre, class PV>
+__device__ __forceinline__ void load_pre(int P, int row1, int S, Pre pre, PV (&ad)[RW]) {
     const int st = min((int)(threadIdx.x & 63) % G, S - 1);
 #pragma unroll
     for (int r = 0; r < RW; r++) ad[r] = pre(st, min(prow<G>(P, r), row1 - 1));
 }
 
 // Row sums over the lane groups; lane s of a group runs the epilogue of state s.
-template <int G, class Epi>
+template <int G, class PV, class Epi>
 __device__ __forceinline__ void finish(int P, int nr, int row1, int S, unsigned amask, float (&acc)[RW][SMAX],
-                                       const float2 (&ad)[RW], Epi epi) {
+                                       const PV (&ad)[RW], Epi epi) {
     const int gl = (int)(threadIdx.x & 63) % G;
 #pragma unroll
     for (int r = 0; r < RW; r++) {
@@ -476,7 +573,7 @@ __device__ __forceinline__ void gemv(const MatView &w, int row0, int row1, int S
     };
     Blk b0[RW], b1[RW], b2[RW];
     float acc[RW][SMAX];
-    float2 ad[RW];
+    decltype(pre(0, 0)) ad[RW];
     unit(0, b0);
     unit(min(1, NU - 1), b1);
     load_pre<G>(row0, row1, S, pre, ad);
@@ -504,15 +601,16 @@ __device__ __forceinline__ void gemv(const MatView &w, int row0, int row1, int S
 }
 
 // Rows [row0, row1) of w when the S states' input rows do not fit in LDS: passes
-// over the columns, staged from src; each wave keeps its rows' sums across the
-// passes (the host sizes the grid so a workgroup has at most one pass of rows).
-template <int TYPE, int G, class Src, class Pre, class Epi>
-__device__ __forceinline__ void gemv_cols(const MatView &w, int row0, int row1, int S, unsigned amask, Src src,
+// over the columns, staged by fillc(c0, nbc); each wave keeps its rows' sums
+// across the passes (the host sizes the grid so a workgroup has at most one pass
+// of rows).
+template <int TYPE, int G, class FillC, class Pre, class Epi>
+__device__ __forceinline__ void gemv_cols(const MatView &w, int row0, int row1, int S, unsigned amask, FillC fillc,
                                           const Lds &L, Pre pre, Epi epi) {
     if (row0 >= row1) return;
     const int nb = w.nb, per = XBLK / S, gl = (int)(threadIdx.x & 63) % G;
     const int nr = pslots<G>(row0, row1);
-    float2 ad[RW];
+    decltype(pre(0, 0)) ad[RW];
     load_pre<G>(row0, row1, S, pre, ad);
     float acc[RW][SMAX];
 #pragma unroll
@@ -521,7 +619,7 @@ __device__ __forceinline__ void gemv_cols(const MatView &w, int row0, int row1, 
         for (int s = 0; s < SMAX; s++) acc[r][s] = 0.0f;
     for (int c0 = 0; c0 < nb; c0 += per) {
         const int nbc = min(per, nb - c0);
-        stage_cols(S, w.cols, c0, nbc, src, L.xs, L.sx, TYPE != 8);
+        stage_cols(S, nbc, [&]() __attribute__((always_inline)) { fillc(c0, nbc); }, L.xs, L.sx, TYPE != 8);
         if (nr > 0)
             for (int b = gl; b < nbc; b += G) {
                 Blk rb[RW];
@@ -534,22 +632,34 @@ __device__ __forceinline__ void gemv_cols(const MatView &w, int row0, int row1, 
     __syncthreads();
 }
 
-// All columns staged from src when they fit, else column passes.
-template <int TYPE, int G, class Src, class Pre, class Epi>
-__device__ __forceinline__ void gemv_src(const MatView &w, int row0, int row1, int S, unsigned amask, Src src,
+// All columns staged by fillc when they fit, else column passes.
+template <int TYPE, int G, class FillC, class Pre, class Epi>
+__device__ __forceinline__ void gemv_src(const MatView &w, int row0, int row1, int S, unsigned amask, FillC fillc,
                                          const Lds &L, Pre pre, Epi epi) {
     if (w.nb <= XBLK / S)
         gemv<TYPE, G>(
             w, row0, row1, S, amask,
-            [&]() __attribute__((always_inline)) { stage_cols(S, w.cols, 0, w.nb, src, L.xs, L.sx, TYPE != 8); }, L,
-            pre, epi);
+            [&]() __attribute__((always_inline)) {
+                stage_cols(S, w.nb, [&]() __attribute__((always_inline)) { fillc(0, w.nb); }, L.xs, L.sx, TYPE != 8);
+            },
+            L, pre, epi);
     else
-        gemv_cols<TYPE, G>(w, row0, row1, S, amask, src, L, pre, epi);
+        gemv_cols<TYPE, G>(w, row0, row1, S, amask, fillc, L, pre, epi);
 }
 
 __device__ __forceinline__ int split(int n, int w, int W) { return (int)((long)n * w / W); }
 
 // ---- the step ------------------------------------------------------------------------------
+// epilogue operands: pairs already loaded, checked for their tag when used
+struct PreXS {  // x and sa_l of the row, the bias
+    uint64_t x, sa;
+    float b;
+};
+struct PreX2 {  // x2 of the row, the bias
+    uint64_t x2;
+    float b;
+};
+
 // G: lanes per row group, 32 for models of width <= 1024, else 64
 template <int TYPE, int G>
 __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
@@ -571,7 +681,7 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
     }
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     // the phase counter continues from this workgroup's last published phase (every
-    // workgroup passes the same barriers, so all start from the same value)
+    // workgroup advances it alike, so all start from the same value)
     unsigned *const flags = a.flags, *const errw = a.err;
     unsigned g = __hip_atomic_load(flags + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     unsigned amask = 0;
@@ -586,27 +696,43 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
 
     const int ctx = a.ctx, enc_len = a.enc_len;
     const size_t kvs = a.kv_stream, plane = (size_t)H * ctx * 64;
-    float *xg = a.x, *x2g = a.x2, *qg = a.q, *hg = a.h, *sag = a.sa;
+    uint64_t *const xg = a.x, *const x2g = a.x2, *const qg = a.q, *const hg = a.h, *const atg = a.attn;
+    uint64_t *const sag = a.sa;
     const int *posl = L.pos;
     const auto nopre = [](int, int) { return make_float2(0.f, 0.f); };
-    // rows of this layer's self-attention output sa_l = Wo V0 + bo (V0: KV row 0)
-    const auto sa_rows = [&](const BLayer *ly, float *sal, int r0, int r1) __attribute__((always_inline)) {
+    // staging of [S][cols] pair vectors (rows ld apart), tags >= t
+    const auto fill_pairs = [&](const uint64_t *v, unsigned t, size_t ld, int cols) __attribute__((always_inline)) {
+        return [=](int c0, int nbc) __attribute__((always_inline)) {
+            burst_pairs<PU, false>(S, amask, cols, c0, nbc, v, t, nullptr, 0, ld, L.xs, errw);
+        };
+    };
+    // rows of this layer's self-attention output sa_l = Wo V0 + bo (V0: KV row 0), tag t
+    const auto sa_rows = [&](const BLayer *ly, uint64_t *sal, int r0, int r1, unsigned t) __attribute__((always_inline)) {
         const float *vp = ly->kv + plane;
         const float *sob = ly->sob;
         gemv_src<TYPE, G>(
             ly->so, r0, r1, S, amask,
-            [=](int s, int c) { return ldx4(vp + (size_t)s * kvs + (size_t)(c >> 6) * ctx * 64 + (c & 63)); }, L,
-            [=](int, int r) { return make_float2(0.f, ldg(sob + r)); },
-            [=](int s, int r, float v, float2 p) { stx(sal + (size_t)s * d + r, v + p.y); });
+            [&](int c0, int nbc) __attribute__((always_inline)) {
+                burst(S, d, c0, nbc,
+                      [=](int s, int c) { return ldx4(vp + (size_t)s * kvs + (size_t)(c >> 6) * ctx * 64 + (c & 63)); },
+                      L.xs);
+            },
+            L, [=](int, int r) { return make_float2(0.f, ldg(sob + r)); },
+            [=](int s, int r, float v, float2 p) { stp(sal + (size_t)s * d + r, v + p.y, t); });
     };
-    // k,v rows [d + r0, d + r1) of the stacked q,k,v matrix into the KV cache at pos
-    const auto kv_rows = [&](const BLayer *ly, int r0, int r1) __attribute__((always_inline)) {
-        const float *xr = xg, *lw = ly->ln1w, *lb = ly->ln1b;
+    // k,v rows [d + r0, d + r1) of the stacked q,k,v matrix into the KV cache at pos,
+    // from LN1 of x (tag tx)
+    const auto kv_rows = [&](const BLayer *ly, int r0, int r1, unsigned tx) __attribute__((always_inline)) {
+        const float *lw = ly->ln1w, *lb = ly->ln1b;
         float *kv = ly->kv;
         const float *svb = ly->svb;
         gemv<TYPE, G>(ly->sqkv, d + r0, d + r1, S, amask,
                    [&]() __attribute__((always_inline)) {
-                       stage_ln(S, d, [=](int s, int c) { return ldx4(xr + (size_t)s * d + c); }, lw, lb, L, TYPE != 8);
+                       stage_ln(S, d,
+                                [&]() __attribute__((always_inline)) {
+                                    burst_pairs<PU, false>(S, amask, d, 0, d / 32, xg, tx, nullptr, 0, d, L.xs, errw);
+                                },
+                                lw, lb, L, TYPE != 8);
                    }, L,
                    [=](int, int r) { return make_float2(0.f, r >= 2 * d ? ldg(svb + r - 2 * d) : 0.0f); },
                    [=](int s, int r, float v, float2 p) {
@@ -616,58 +742,63 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
                            v + p.y);
                    });
     };
-    // cross query rows [r0, r1) from LN2(x + sa_l)
-    const auto cq_rows = [&](const BLayer *ly, const float *sal, int r0, int r1) __attribute__((always_inline)) {
-        const float *xr = xg, *lw = ly->ln2w, *lb = ly->ln2b;
+    // cross query rows [r0, r1) from LN2(x + sa_l) (tags tx, tsa) into q (tag t)
+    const auto cq_rows = [&](const BLayer *ly, const uint64_t *sal, int r0, int r1, unsigned tx, unsigned tsa,
+                             unsigned t) __attribute__((always_inline)) {
+        const float *lw = ly->ln2w, *lb = ly->ln2b;
         const float *cqb = ly->cqb;
-        float *qw = qg;
         gemv<TYPE, G>(ly->cq, r0, r1, S, amask,
                    [&]() __attribute__((always_inline)) {
-                       stage_ln(
-                           S, d,
-                           [=](int s, int c) {
-                               const float4 u = ldx4(xr + (size_t)s * d + c), v = ldx4(sal + (size_t)s * d + c);
-                               return make_float4(u.x + v.x, u.y + v.y, u.z + v.z, u.w + v.w);
-                           },
-                           lw, lb, L, TYPE != 8);
+                       stage_ln(S, d,
+                                [&]() __attribute__((always_inline)) {
+                                    burst_pairs<PU2, true>(S, amask, d, 0, d / 32, xg, tx, sal, tsa, d, L.xs, errw);
+                                },
+                                lw, lb, L, TYPE != 8);
                    }, L, [=](int, int r) { return make_float2(0.f, ldg(cqb + r)); },
-                   [=](int s, int r, float v, float2 p) { stx(qw + (size_t)s * d + r, v + p.y); });
+                   [=](int s, int r, float v, float2 p) { stp(qg + (size_t)s * d + r, v + p.y, t); });
     };
 
     // embedding (decoder.go:756-773): the quantised row is dequantised bit-exactly
+    const unsigned tE = ++g;
     for (int i = split(S * d, w, W) + threadIdx.x; i < split(S * d, w + 1, W); i += NT) {
         const int s = i / d, e = i % d;
         if (!((amask >> s) & 1u)) continue;
-        stx(xg + i, dequant_elem<TYPE>(a.tok, a.tokv[s], e >> 5, e & 31) + ldg(a.pos_emb + (size_t)posl[s] * d + e));
+        stp(xg + i, dequant_elem<TYPE>(a.tok, a.tokv[s], e >> 5, e & 31) + ldg(a.pos_emb + (size_t)posl[s] * d + e),
+            tE);
     }
     // past position 0 every layer's sa_l is known now: its rows for all layers
     if (!pos0) {
         const int r0 = split(Ln * d, w, W), r1 = split(Ln * d, w + 1, W);
         for (int l = r0 / d; l < Ln && l * d < r1; l++)
-            sa_rows(lyl + l, sag + (size_t)l * S * d, max(r0, l * d) - l * d, min(r1, (l + 1) * d) - l * d);
+            sa_rows(lyl + l, sag + (size_t)l * S * d, max(r0, l * d) - l * d, min(r1, (l + 1) * d) - l * d, tE);
     }
-    gbar(flags, errw, g);
+    __syncthreads();
 
-    // after a failed wait every barrier returns at once: the launch runs out and the
+    // after a failed wait every wait returns at once: the launch runs out and the
     // host reports the failure
     const int Wk = W - W / 3;  // k,v workgroups of phase B
+    unsigned tx = tE;          // tag of the current x
     for (int l = 0; l < Ln; l++) {
         const BLayer *ly = lyl + l;
-        float *sal = sag + (size_t)l * S * d;
+        uint64_t *sal = sag + (size_t)l * S * d;
         // ---- B: k,v rows; cross query rows ----
+        unsigned tsa = tE, tq;
         if (pos0) {
-            kv_rows(ly, split(2 * d, w, W), split(2 * d, w + 1, W));
-            gbar(flags, errw, g);
-            sa_rows(ly, sal, split(d, w, W), split(d, w + 1, W));
-            gbar(flags, errw, g);
-            cq_rows(ly, sal, split(d, w, W), split(d, w + 1, W));
-        } else if (w < Wk) {
-            kv_rows(ly, split(2 * d, w, Wk), split(2 * d, w + 1, Wk));
+            kv_rows(ly, split(2 * d, w, W), split(2 * d, w + 1, W), tx);
+            gbar(flags, errw, g);  // V0 is read as plain floats next
+            tsa = ++g;
+            sa_rows(ly, sal, split(d, w, W), split(d, w + 1, W), tsa);
+            tq = ++g;
+            cq_rows(ly, sal, split(d, w, W), split(d, w + 1, W), tx, tsa, tq);
         } else {
-            cq_rows(ly, sal, split(d, w - Wk, W - Wk), split(d, w + 1 - Wk, W - Wk));
+            tq = ++g;
+            if (w < Wk)
+                kv_rows(ly, split(2 * d, w, Wk), split(2 * d, w + 1, Wk), tx);
+            else
+                cq_rows(ly, sal, split(d, w - Wk, W - Wk), split(d, w + 1 - Wk, W - Wk), tx, tsa, tq);
         }
-        gbar(flags, errw, g);
         // ---- X: cross attention; item (state, head, key chunk) on workgroup w ----
+        const unsigned tX = ++g;
         {
             // one item per workgroup when they fit the grid; else XC is 1 and a
             // workgroup takes whole heads one after another (no exchange to wait on)
@@ -679,7 +810,13 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
                 constexpr int XS = 12;       // steps per batch
                 const int q16 = lane & 15, kq = wv * 4 + (lane >> 4);  // the lane's key of a step
                 const size_t sh = (size_t)s * H + h;
-                const float4 q4 = ldx4(qg + (size_t)s * d + h * 64 + q16 * 4);
+                float4 q4;
+                {
+                    const uint64_t *qp = qg + (size_t)s * d + h * 64 + q16 * 4;
+                    const uint64_t v0 = ldp(qp), v1 = ldp(qp + 1), v2 = ldp(qp + 2), v3 = ldp(qp + 3);
+                    q4 = make_float4(waitp(qp, v0, tq, errw), waitp(qp + 1, v1, tq, errw), waitp(qp + 2, v2, tq, errw),
+                                     waitp(qp + 3, v3, tq, errw));
+                }
                 const float *K = (const float *)((gcu64 *)ly->kbase)[s] + (size_t)h * enc_len * 64;
                 const float *V = (const float *)((gcu64 *)ly->vbase)[s] + (size_t)h * enc_len * 64;
                 const int t0 = c * klen, t1 = min(t0 + klen, enc_len);
@@ -726,26 +863,13 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
                 __syncthreads();
                 float M = L.red[0];
                 for (int i = 1; i < NWV; i++) M = fmaxf(M, L.red[i]);
-                // the head maximum: the chunk maxima of the head's workgroups, exchanged as
-                // {phase, value} pairs (no grid barrier)
+                // the head maximum: the chunk maxima of the head's workgroups
                 if (XC > 1) {
-                    if (threadIdx.x == 0)
-                        __hip_atomic_store((gu64 *)(a.xmax + it), ((uint64_t)g << 32) | __float_as_uint(M),
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (threadIdx.x == 0) stp(a.xmax + it, M, tX);
                     if (threadIdx.x < 64) {
-                        gcu64 *src = (gcu64 *)(a.xmax + sh * XC);
+                        const uint64_t *src = a.xmax + sh * XC;
                         const int li = min(lane, XC - 1);
-                        uint64_t v = __hip_atomic_load(src + li, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        for (unsigned spins = 0;; spins++) {
-                            if (__all((unsigned)(v >> 32) >= g)) break;
-                            if (__any(failed(errw) || spins > SPIN_MAX)) {
-                                if (lane == 0) atomicOr(errw, 1u);
-                                break;
-                            }
-                            if ((unsigned)(v >> 32) < g)
-                                v = __hip_atomic_load(src + li, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        }
-                        const float m = wmax(__uint_as_float((uint32_t)v));
+                        const float m = wmax(waitp(src + li, ldp(src + li), tX, errw));
                         if (lane == 0) L.red[8] = m;
                     }
                     __syncthreads();
@@ -782,6 +906,7 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
                 }
                 es = wsum(es);
                 float4 *red4 = (float4 *)(L.red + 64);  // [NWV][16]
+                float *own = L.red + 640;              // the chunk's P.V [64] and weight sum [64]
                 if (lane < 16) red4[wv * 16 + lane] = acc;
                 if (lane == 0) L.red[16 + wv] = es;
                 __syncthreads();
@@ -791,99 +916,115 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
                         const float4 t4 = red4[i * 16 + threadIdx.x];
                         r.x += t4.x; r.y += t4.y; r.z += t4.z; r.w += t4.w;
                     }
-                    float *dst = a.pv + (size_t)it * 64 + threadIdx.x * 4;
-                    stx(dst, r.x); stx(dst + 1, r.y); stx(dst + 2, r.z); stx(dst + 3, r.w);
+                    *(float4 *)(own + 4 * threadIdx.x) = r;
                 }
                 if (threadIdx.x == 0) {
                     float t = 0.0f;
                     for (int i = 0; i < NWV; i++) t += L.red[16 + i];
-                    stx(a.psum + it, t);
+                    own[64] = t;
+                }
+                __syncthreads();
+                uint64_t *at = atg + (size_t)s * d + h * 64;
+                if (XC == 1) {
+                    if (threadIdx.x < 64) stp(at + threadIdx.x, own[threadIdx.x] * (1.0f / own[64]), tX);
+                } else {
+                    // the chunk's P.V and weight sum; the head's first chunk adds the
+                    // others' in chunk order: attn = sum P.V * (1 / sum of weight sums)
+                    if (threadIdx.x < 65) stp(a.pv + (size_t)it * 65 + threadIdx.x, own[threadIdx.x], tX);
+                    if (c == 0) {
+                        // thread t: element t % 65 (P.V columns, then the weight sum) of
+                        // chunk 1 + t / 65, into LDS; then lane j adds column j in chunk order
+                        float *oth = scl;  // [XC - 1][65], over the chunk's scores (used up)
+                        const int t = threadIdx.x;
+                        if (t < (XC - 1) * 65) {
+                            const uint64_t *pp = a.pv + ((size_t)it + 1) * 65 + t;
+                            oth[t] = waitp(pp, ldp(pp), tX, errw);
+                        }
+                        __syncthreads();
+                        if (t < 64) {
+                            float o = own[t], sum = own[64];
+                            for (int i = 1; i < XC; i++) {
+                                o += oth[(i - 1) * 65 + t];
+                                sum += oth[(i - 1) * 65 + 64];
+                            }
+                            stp(at + t, o * (1.0f / sum), tX);
+                        }
+                    }
                 }
                 __syncthreads();  // LDS scores and reduction area free for the next item
             }
             }
         }
-        gbar(flags, errw, g);
-        // ---- F: cross out rows on the combined heads; x2 = (x + sa_l) + (Wo_c.attn + b) ----
+        // ---- F: cross out rows; x2 = (x + sa_l) + (Wo_c.attn + b) ----
+        const unsigned tF = ++g;
         {
-            const float *cob = ly->cob, *xr = xg, *pvr = a.pv, *psr = a.psum;
-            float *x2w = x2g;
-            const int XC = a.xchunks;
+            const float *cob = ly->cob;
             gemv_src<TYPE, G>(
-                ly->co, split(d, w, W), split(d, w + 1, W), S, amask,
-                [=](int s, int c) {
-                    // head h of state s: its chunks' P.V over their weight sums
-                    const size_t b = ((size_t)s * H + (c >> 6)) * XC;
-                    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-                    float sum = 0.0f;
-                    // the chunks' loads go out together, then the sums
-                    float4 p4[CMAX];
-                    float ps[CMAX];
-#pragma unroll
-                    for (int i = 0; i < CMAX; i++)
-                        if (i < XC) {
-                            p4[i] = ldx4(pvr + (b + i) * 64 + (c & 63));
-                            ps[i] = ldx(psr + b + i);
-                        }
-#pragma unroll
-                    for (int i = 0; i < CMAX; i++)
-                        if (i < XC) {
-                            o.x += p4[i].x; o.y += p4[i].y; o.z += p4[i].z; o.w += p4[i].w;
-                            sum += ps[i];
-                        }
-                    const float inv = 1.0f / sum;
-                    return make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
-                },
-                L,
+                ly->co, split(d, w, W), split(d, w + 1, W), S, amask, fill_pairs(atg, tX, d, d), L,
                 [=](int s, int r) {
-                    return make_float2(ldx(xr + (size_t)s * d + r) + ldx(sal + (size_t)s * d + r), ldg(cob + r));
+                    return PreXS{ldp(xg + (size_t)s * d + r), ldp(sal + (size_t)s * d + r), ldg(cob + r)};
                 },
-                [=](int s, int r, float v, float2 p) { stx(x2w + (size_t)s * d + r, p.x + (v + p.y)); });
+                [=](int s, int r, float v, PreXS p) {
+                    const float xv = waitp(xg + (size_t)s * d + r, p.x, tx, errw);
+                    const float sv = waitp(sal + (size_t)s * d + r, p.sa, tsa, errw);
+                    stp(x2g + (size_t)s * d + r, (xv + sv) + (v + p.b), tF);
+                });
         }
-        gbar(flags, errw, g);
         // ---- G: LN3, fc1 rows + GELU ----
+        const unsigned tG = ++g;
         {
             const int r0 = split(4 * d, w, W), r1 = split(4 * d, w + 1, W);
             if (r0 < r1) {
-                const float *x2r = x2g, *fc1b = ly->fc1b, *lw = ly->ln3w, *lb = ly->ln3b;
-                float *hw = hg;
+                const float *fc1b = ly->fc1b, *lw = ly->ln3w, *lb = ly->ln3b;
                 gemv<TYPE, G>(ly->fc1, r0, r1, S, amask,
                            [&]() __attribute__((always_inline)) {
-                               stage_ln(S, d, [=](int s, int c) { return ldx4(x2r + (size_t)s * d + c); }, lw, lb, L,
-                                        TYPE != 8);
+                               stage_ln(S, d,
+                                        [&]() __attribute__((always_inline)) {
+                                            burst_pairs<PU, false>(S, amask, d, 0, d / 32, x2g, tF, nullptr, 0, d, L.xs,
+                                                                  errw);
+                                        },
+                                        lw, lb, L, TYPE != 8);
                            }, L,
                            [=](int, int r) { return make_float2(0.f, ldg(fc1b + r)); },
-                           [=](int s, int r, float v, float2 p) { stx(hw + (size_t)s * 4 * d + r, gelu_ref(v + p.y)); });
+                           [=](int s, int r, float v, float2 p) {
+                               stp(hg + (size_t)s * 4 * d + r, gelu_ref(v + p.y), tG);
+                           });
             }
         }
-        gbar(flags, errw, g);
         // ---- H: fc2 rows; x = x2 + (W2.h + b2) ----
+        const unsigned tH = ++g;
         {
-            const float *fc2b = ly->fc2b, *hr = hg, *x2r = x2g;
-            float *xw = xg;
+            const float *fc2b = ly->fc2b;
             gemv_src<TYPE, G>(
-                ly->fc2, split(d, w, W), split(d, w + 1, W), S, amask,
-                [=](int s, int c) { return ldx4(hr + (size_t)s * 4 * d + c); }, L,
-                [=](int s, int r) { return make_float2(ldx(x2r + (size_t)s * d + r), ldg(fc2b + r)); },
-                [=](int s, int r, float v, float2 p) { stx(xw + (size_t)s * d + r, p.x + (v + p.y)); });
+                ly->fc2, split(d, w, W), split(d, w + 1, W), S, amask, fill_pairs(hg, tG, (size_t)4 * d, 4 * d), L,
+                [=](int s, int r) { return PreX2{ldp(x2g + (size_t)s * d + r), ldg(fc2b + r)}; },
+                [=](int s, int r, float v, PreX2 p) {
+                    stp(xg + (size_t)s * d + r, waitp(x2g + (size_t)s * d + r, p.x2, tF, errw) + (v + p.b), tH);
+                });
         }
-        gbar(flags, errw, g);
+        tx = tH;
     }
     // ---- final LayerNorm and tied logits rows (decoder.go:817-832) ----
     {
         const int r0 = split(a.V, w, W), r1 = split(a.V, w + 1, W);
         if (r0 < r1) {
-            const float *xr = xg, *lw = a.lnw, *lb = a.lnb;
+            const float *lw = a.lnw, *lb = a.lnb;
             float *lg = a.logits;
             const int V = a.V;
             gemv<TYPE, G>(a.tok, r0, r1, S, amask,
                        [&]() __attribute__((always_inline)) {
-                           stage_ln(S, d, [=](int s, int c) { return ldx4(xr + (size_t)s * d + c); }, lw, lb, L,
-                                    TYPE != 8);
+                           stage_ln(S, d,
+                                    [&]() __attribute__((always_inline)) {
+                                        burst_pairs<PU, false>(S, amask, d, 0, d / 32, xg, tx, nullptr, 0, d, L.xs,
+                                                              errw);
+                                    },
+                                    lw, lb, L, TYPE != 8);
                        }, L, nopre,
                        [=](int s, int r, float v, float2) { stg(lg + (size_t)s * V + r, v); });
         }
     }
+    // the next launch continues from this phase
+    if (threadIdx.x == 0) __hip_atomic_store(flags + w, g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Launch of the kernel for weight type TYPE; G from the model width.

@@ -489,13 +489,17 @@ int batch_setup(wh_seq &s) {
     a.tok = view(m.tok);
     a.pos_emb = m.pos; a.lnw = m.lnw; a.lnb = m.lnb;
     a.tokv = s.tok; a.posv = s.pos; a.active = s.active;
-    a.x = s.x; a.q = s.q; a.h = s.h; a.logits = s.logits;
-    const size_t items = (size_t)s.S * H * xchunks;
-    if ((rc = s.alloc(&a.x2, (size_t)s.S * d)) || (rc = s.alloc(&a.sa, (size_t)L * s.S * d)) ||
-        (rc = s.alloc(&a.pv, items * 64)) || (rc = s.alloc(&a.psum, items)) || (rc = s.alloc(&a.xmax, items)) ||
-        (rc = s.alloc(&a.flags, (size_t)W)) || (rc = s.alloc(&a.err, 1)))
-        return rc;
-    WH_HIP(hipMemsetAsync(a.xmax, 0, sizeof(uint64_t) * items, s.st));
+    a.logits = s.logits;
+    // the exchanged {tag, value} pairs start with tag 0, below every phase's tag
+    const size_t items = (size_t)s.S * H * xchunks, sd = (size_t)s.S * d;
+    struct { uint64_t **p; size_t n; } pairs[] = {{&a.x, sd},      {&a.x2, sd},         {&a.q, sd},
+                                                  {&a.h, 4 * sd},  {&a.attn, sd},       {&a.sa, (size_t)L * sd},
+                                                  {&a.pv, items * 65}, {&a.xmax, items}};
+    for (auto &b : pairs) {
+        if ((rc = s.alloc(b.p, b.n))) return rc;
+        WH_HIP(hipMemsetAsync(*b.p, 0, sizeof(uint64_t) * b.n, s.st));
+    }
+    if ((rc = s.alloc(&a.flags, (size_t)W)) || (rc = s.alloc(&a.err, 1))) return rc;
     WH_HIP(hipMemsetAsync(a.flags, 0, sizeof(unsigned) * W, s.st));
     WH_HIP(hipMemsetAsync(a.err, 0, sizeof(unsigned), s.st));
     a.scale = (float)(1.0 / sqrt(64.0));
