@@ -443,7 +443,7 @@ def run_gemv(args):
                 h = C.c_void_p()
                 wh.native.check(lib.wh_matrix_create(qt, rows, cols, raw.ctypes.data, raw.size, 0, C.byref(h)))
                 mats.append(h)
-            for batch in (1, 5):
+            for batch in [int(b) for b in args.gemv_batches.split(",")]:
                 x = wh.native.DevBuf.from_array(rng.standard_normal((batch, cols)).astype(np.float32))
                 y = wh.native.DevBuf(batch * rows * 4)
                 for h in mats[:4]:
@@ -505,6 +505,7 @@ def main():
                          "encoder forward of --config in --qtype")
     ap.add_argument("--encoder-steps", type=int, default=10, help="timed encodes of the encoder workload")
     ap.add_argument("--gemv-formats", default="Q8_0,Q4_0,Q4_1,Q5_0,Q5_1")
+    ap.add_argument("--gemv-batches", default="1,5", help="GEMV microbench: batch sizes (up to 16)")
     ap.add_argument("--gemv-single", action="store_true",
                     help="GEMV microbench: single launches between event pairs only, no graph "
                          "(for kernel-trace profiling)")
