@@ -7,7 +7,8 @@ both sides). Covers quantised and float weights, head size 64 (the tiled
 attention kernel) and another head size (the generic one), odd frame counts,
 the stored weight orders and HF names the reference accepts, GGUF files with
 and without metadata, the frame-count rules, cancellation, the full-size
-tiny.en encoder, and mel -> encoder -> decoder tokens end to end.
+tiny.en encoder, the large-v3 shapes over a full window, and mel -> encoder ->
+decoder tokens end to end.
 """
 import ctypes as C
 
@@ -176,6 +177,22 @@ def test_tiny_en_full_size_vs_oracle(wh, orc, gpu):
     want = orc.OracleEncoder(tensors, meta, threads=16).encode(mel)
     assert got.shape == want.shape == (1500, 384)
     print(f"tiny.en encoder rel err {_rel(got, want):.3g}", flush=True)
+    assert _rel(got, want) < TOL
+
+
+def test_large_v3_shape_vs_oracle(wh, orc, gpu):
+    """The large-v3 encoder's shapes (128 mels, d = 1280, 20 heads) over a full
+    window of 3000 frames -> 1500 rows, with its first block only (every block
+    runs the same kernels at the same sizes), Q8_0, against the oracle."""
+    dims = (128, 1280, 20, 1, 1500)
+    tensors, meta = wh.synth.make_encoder("large-v3", 8, dims=dims)
+    mel = wh.synth.mel_input("large-v3", 128, T=3000)
+    enc = wh.HIPEncoder(tensors, meta)
+    got = enc.encode(mel)
+    enc.close()
+    want = orc.OracleEncoder(tensors, meta, threads=16).encode(mel)
+    assert got.shape == want.shape == (1500, 1280)
+    print(f"large-v3 shape encoder rel err {_rel(got, want):.3g}", flush=True)
     assert _rel(got, want) < TOL
 
 

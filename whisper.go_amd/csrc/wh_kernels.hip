@@ -1982,26 +1982,45 @@ __global__ __launch_bounds__(256) void k_beam_select(const int32_t *ttok, const 
     __shared__ float cnorm[NCAND], cscore[NCAND], clp[NCAND];
     __shared__ int cpar[NCAND], ctok[NCAND], cix[NCAND];
     __shared__ int reuse[BEAM_MAX], next[BEAM_MAX];
+    // the beam objects' state, read once by as many threads: length, capacity,
+    // last token (kept current as the slots below are applied in place), score,
+    // and the candidates of the top-k
+    __shared__ int blen[BEAM_MAX], bcap[BEAM_MAX], blast[BEAM_MAX], border[BEAM_MAX];
+    __shared__ float bscore[BEAM_MAX];
+    __shared__ float tlps[BEAM_MAX * TOPK_MAX];
+    __shared__ int ttoks[BEAM_MAX * TOPK_MAX];
     __shared__ int nkeep, nbin, s_nb, s_par, s_cpy, s_zero, s_bad;
     const int t = threadIdx.x;
     if (stop[0]) return;
+    if (t < bs) {
+        blen[t] = len[t];
+        bcap[t] = gcap[t];
+        bscore[t] = score[t];
+        border[t] = order[t];
+    }
+    for (int i = t; i < bs * kk; i += blockDim.x) {
+        tlps[i] = tlp[i];
+        ttoks[i] = ttok[i];
+    }
+    __syncthreads();
+    if (t < bs) blast[t] = blen[t] > 0 ? hist[(size_t)t * cap + blen[t] - 1] : -1;
+    __syncthreads();
     if (t == 0) {
         const int nb = *nbeams;
         int n = 0;
         for (int b = 0; b < nb; b++) {
-            const int o = order[b];
+            const int o = border[b];
             reuse[b] = o;
-            const int L = len[o];
-            const int last = L > 0 ? hist[(size_t)o * cap + L - 1] : -1;
-            const float sc = score[o];
-            if (last == eot) {
+            const int L = blen[o];
+            const float sc = bscore[o];
+            if (blast[o] == eot) {
                 cpar[n] = o; cscore[n] = sc; ctok[n] = eot; clp[n] = 0.0f; cnorm[n] = sc / powtab[L];
                 n++;
             } else {
                 for (int c = 0; c < k; c++) {
-                    const float lpc = tlp[(size_t)o * kk + c];
+                    const float lpc = tlps[o * kk + c];
                     const float ns = sc + lpc;
-                    cpar[n] = o; cscore[n] = ns; ctok[n] = ttok[(size_t)o * kk + c]; clp[n] = lpc;
+                    cpar[n] = o; cscore[n] = ns; ctok[n] = ttoks[o * kk + c]; clp[n] = lpc;
                     cnorm[n] = ns / powtab[L + 1];
                     n++;
                 }
@@ -2020,19 +2039,19 @@ __global__ __launch_bounds__(256) void k_beam_select(const int32_t *ttok, const 
             const int c = cix[i];
             const int o = reuse[nbin - 1 - i];  // reusableBeams[n-1], popped
             const int par = cpar[c];
-            const int L = len[par];
-            const int last = L > 0 ? hist[(size_t)par * cap + L - 1] : -1;
-            const bool carry = last == eot && ctok[c] == eot && clp[c] == 0.0f;
+            const int L = blen[par];
+            const bool carry = blast[par] == eot && ctok[c] == eot && clp[c] == 0.0f;
             const int need = carry ? L : L + 1;
             // make([]int32, need) when the capacity is short; a self-parent then copies the zeros
-            s_zero = (gcap[o] < need && o == par) ? need : 0;
-            if (gcap[o] < need) gcap[o] = need;
+            s_zero = (bcap[o] < need && o == par) ? need : 0;
+            if (bcap[o] < need) bcap[o] = need;
             s_cpy = (o != par) ? (carry ? need : need - 1) : 0;
             s_nb = o;
             s_par = par;
             next[i] = o;
-            len[o] = need;
-            score[o] = cscore[c];
+            blen[o] = need;
+            bscore[o] = cscore[c];
+            blast[o] = carry ? eot : ctok[c];
             // the appended token (written after the copy below)
             cix[i] = carry ? -1 : ctok[c];
         }
@@ -2041,16 +2060,21 @@ __global__ __launch_bounds__(256) void k_beam_select(const int32_t *ttok, const 
         for (int j = t; j < nz; j += blockDim.x) hist[(size_t)o * cap + j] = 0;
         for (int j = t; j < nc; j += blockDim.x) hist[(size_t)o * cap + j] = hist[(size_t)par * cap + j];
         __syncthreads();
-        if (t == 0 && cix[i] >= 0) hist[(size_t)o * cap + len[o] - 1] = cix[i];
+        if (t == 0 && cix[i] >= 0) hist[(size_t)o * cap + blen[o] - 1] = cix[i];
         __syncthreads();
+    }
+    if (t < bs) {
+        len[t] = blen[t];
+        gcap[t] = bcap[t];
+        score[t] = bscore[t];
     }
     if (t == 0) {
         int bad_pos = -1;
         for (int i = 0; i < keep; i++) {
             const int o = next[i];
             order[i] = o;
-            const int L = len[o];
-            const int lt = L > 0 ? hist[(size_t)o * cap + L - 1] : -1;
+            const int L = blen[o];
+            const int lt = L > 0 ? blast[o] : -1;
             tok[o] = lt;
             pos[o] = L - 1;
             const bool live = lt != eot;
@@ -2061,14 +2085,14 @@ __global__ __launch_bounds__(256) void k_beam_select(const int32_t *ttok, const 
         for (int i = keep; i < nbin; i++) active[reuse[nbin - 1 - i]] = 0;
         *nbeams = keep;
         bool all = true;
-        for (int i = 0; i < keep; i++) all &= (tok[next[i]] == eot);
+        for (int i = 0; i < keep; i++) all &= (blast[next[i]] == eot);
         bool halt = all || keep == 0;
         if (!halt && keep > 0) {
-            const int o = next[0], L0 = len[o];
+            const int o = next[0], L0 = blen[o];
             const int32_t *h0 = hist + (size_t)o * cap;
             if (L0 >= 2) {
                 int streak = 1;
-                for (int i = L0 - 2; i >= 0 && h0[i] == h0[L0 - 1]; i--)
+                for (int i = L0 - 2; i >= 0 && h0[i] == blast[o]; i--)
                     if (++streak > 20) { halt = true; break; }
             }
         }
