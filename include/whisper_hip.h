@@ -214,6 +214,14 @@ typedef struct {
 int wh_decode(const wh_model *m, const float *encoder_out, int32_t enc_len, int32_t enc_dim,
               const wh_decode_params *params, int32_t *out_tokens, int32_t cap, int32_t *out_len,
               const volatile int32_t *cancel);
+/* The same with encoder_out in device memory of the model's device (for
+ * instance written by wh_encode_device): the cross K/V are projected from it in
+ * place, with no host round trip of the encoder output. No counterpart in the
+ * reference (its tensors live in host memory); WH_ERR_INVALID when the pointer
+ * is not device memory of that device. */
+int wh_decode_device(const wh_model *m, const float *encoder_out, int32_t enc_len, int32_t enc_dim,
+                     const wh_decode_params *params, int32_t *out_tokens, int32_t cap, int32_t *out_len,
+                     const volatile int32_t *cancel);
 
 /* Greedy decode of n_streams independent streams as one batch (each with its
  * own encoder output and prompt). Equivalent to n_streams calls of
@@ -236,6 +244,9 @@ int wh_last_decode_steps(int32_t *out);
 typedef struct wh_seq wh_seq;
 int wh_seq_create(const wh_model *m, int32_t n_streams, const float *const *encoder_outs, int32_t enc_len,
                   int32_t enc_dim, int32_t shared_encoder, wh_seq **out);
+/* The same with the encoder outputs in device memory of the model's device. */
+int wh_seq_create_device(const wh_model *m, int32_t n_streams, const float *const *encoder_outs, int32_t enc_len,
+                         int32_t enc_dim, int32_t shared_encoder, wh_seq **out);
 int wh_seq_destroy(wh_seq *s);
 /* Set the token history of one stream (state.tokens); when reset_kv is non-zero
  * the stream's KV cache is cleared (resetDecoderState, decoder.go:367-386). */

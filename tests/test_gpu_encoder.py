@@ -196,6 +196,31 @@ def test_large_v3_shape_vs_oracle(wh, orc, gpu):
     assert _rel(got, want) < TOL
 
 
+def test_device_encoder_output_feeds_decoder(wh, gpu):
+    """mel -> wh_encode_device -> wh_decode_device, the encoder output never
+    leaving HBM, gives the tokens of the host-buffer path (greedy and beam 3);
+    a host pointer is rejected."""
+    dims_e, dims_d = (16, 128, 2, 2, 60), (600, 128, 2, 2, 48)
+    et, em = wh.synth.make_encoder("edd", 8, dims=dims_e)
+    dt, dm = wh.synth.make_decoder("edd", 8, dims=dims_d)
+    mel = wh.synth.mel_input("edd", 16, T=120)
+    enc, dec = wh.HIPEncoder(et, em), wh.HIPDecoder(dt, dm)
+    host = enc.encode(mel)
+    dmel = wh.native.DevBuf.from_array(mel)
+    dout = wh.native.DevBuf(60 * 128 * 4)
+    rows = enc.encode_device(dmel.ptr.value, 16, 120, dout.ptr.value, 60)
+    assert rows == 60
+    for beam in (1, 3):
+        p = wh.DecoderParams(prompt=[5, 6, 7], beam_size=beam, max_tokens=16, no_fallback=True)
+        assert dec.decode_tokens_device(dout.ptr.value, rows, p) == dec.decode_tokens(host, p), beam
+    with pytest.raises(wh.native.WhError, match="not device memory"):
+        dec.decode_tokens_device(host.ctypes.data, rows, wh.DecoderParams(prompt=[5, 6, 7], max_tokens=4))
+    dmel.free()
+    dout.free()
+    enc.close()
+    dec.close()
+
+
 def test_mel_to_tokens_end_to_end(wh, orc, gpu):
     """mel -> device encoder -> device decoder gives the tokens of mel -> oracle
     encoder -> oracle decoder (greedy and beam 3)."""

@@ -32,7 +32,7 @@ int encode(const wh_encoder *e, const float *mel, int32_t n_mels, int32_t T, flo
 int encode_device(const wh_encoder *e, const float *mel, int32_t n_mels, int32_t T, float *out, int32_t out_cap,
                   int32_t *out_rows, const volatile int32_t *cancel);
 int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t enc_len, int32_t enc_dim, int32_t shared,
-               wh_seq **out);
+               wh_seq **out, int32_t dev);
 int seq_set_tokens(wh_seq *s, int32_t i, const int32_t *tokens, int32_t n, int32_t reset_kv);
 int seq_step_greedy(wh_seq *s, const int32_t *active, float temperature, int32_t suppress_nst, float nst,
                     int32_t *out_ids, float *out_logits);
@@ -47,10 +47,10 @@ int seq_persistent(wh_seq *s, int32_t *out, int64_t *launches);
 int seq_profile_get(wh_seq *s, int32_t i, char *name, int32_t cap, double *ms, int64_t *launches, double *bytes);
 int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, int32_t enc_len, int32_t enc_dim,
                         const wh_decode_params *params, int32_t *out_tokens, int32_t cap, int32_t *out_lens,
-                        const volatile int32_t *cancel);
+                        const volatile int32_t *cancel, int32_t dev);
 int32_t last_decode_steps();
 int decode_beam(const wh_model *m, const float *enc, int32_t enc_len, int32_t enc_dim, const wh_decode_params *p,
-                int32_t *out_tokens, int32_t cap, int32_t *out_len, const volatile int32_t *cancel);
+                int32_t *out_tokens, int32_t cap, int32_t *out_len, const volatile int32_t *cancel, int32_t dev);
 
 // ---- GGUF v2/v3 reader (internal/gguf/gguf.go:52-135, metadata.go, tensor.go) ----
 namespace {
@@ -421,20 +421,32 @@ int wh_decode(const wh_model *m, const float *enc, int32_t enc_len, int32_t enc_
               int32_t *out_tokens, int32_t cap, int32_t *out_len, const volatile int32_t *cancel) {
     if (!m || !enc || !p || !out_tokens || !out_len) return fail(WH_ERR_INVALID, "model: decode: null argument");
     *out_len = 0;
-    if (p->beam_size > 1) return decode_beam(m, enc, enc_len, enc_dim, p, out_tokens, cap, out_len, cancel);
-    return decode_greedy_batch(m, 1, &enc, enc_len, enc_dim, p, out_tokens, cap, out_len, cancel);
+    if (p->beam_size > 1) return decode_beam(m, enc, enc_len, enc_dim, p, out_tokens, cap, out_len, cancel, 0);
+    return decode_greedy_batch(m, 1, &enc, enc_len, enc_dim, p, out_tokens, cap, out_len, cancel, 0);
+}
+
+int wh_decode_device(const wh_model *m, const float *enc, int32_t enc_len, int32_t enc_dim, const wh_decode_params *p,
+                     int32_t *out_tokens, int32_t cap, int32_t *out_len, const volatile int32_t *cancel) {
+    if (!m || !enc || !p || !out_tokens || !out_len) return fail(WH_ERR_INVALID, "model: decode: null argument");
+    *out_len = 0;
+    if (p->beam_size > 1) return decode_beam(m, enc, enc_len, enc_dim, p, out_tokens, cap, out_len, cancel, 1);
+    return decode_greedy_batch(m, 1, &enc, enc_len, enc_dim, p, out_tokens, cap, out_len, cancel, 1);
 }
 
 int wh_decode_batch(const wh_model *m, int32_t n, const float *const *encs, int32_t enc_len, int32_t enc_dim,
                     const wh_decode_params *params, int32_t *out_tokens, int32_t cap, int32_t *out_lens,
                     const volatile int32_t *cancel) {
     if (!m || !encs || !params || !out_tokens || !out_lens) return fail(WH_ERR_INVALID, "model: decode: null argument");
-    return decode_greedy_batch(m, n, encs, enc_len, enc_dim, params, out_tokens, cap, out_lens, cancel);
+    return decode_greedy_batch(m, n, encs, enc_len, enc_dim, params, out_tokens, cap, out_lens, cancel, 0);
 }
 
 int wh_seq_create(const wh_model *m, int32_t n, const float *const *encs, int32_t enc_len, int32_t enc_dim,
                   int32_t shared, wh_seq **out) {
-    return seq_create(m, n, encs, enc_len, enc_dim, shared, out);
+    return seq_create(m, n, encs, enc_len, enc_dim, shared, out, 0);
+}
+int wh_seq_create_device(const wh_model *m, int32_t n, const float *const *encs, int32_t enc_len, int32_t enc_dim,
+                         int32_t shared, wh_seq **out) {
+    return seq_create(m, n, encs, enc_len, enc_dim, shared, out, 1);
 }
 int wh_seq_destroy(wh_seq *s) {
     seq_destroy(s);

@@ -606,8 +606,9 @@ int upload_active(wh_seq &s, const int32_t *active) {
 
 }  // namespace
 
+// encs: host buffers, or (dev) device memory of the model's device, read in place
 int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t enc_len, int32_t enc_dim,
-               int32_t shared, wh_seq **out) {
+               int32_t shared, wh_seq **out, int32_t dev) {
     if (!m || !out) return fail(WH_ERR_INVALID, "seq: null argument");
     *out = nullptr;
     if (S < 1 || S > 16) return fail(WH_ERR_INVALID, "seq: n_streams must be in [1,16]");
@@ -616,6 +617,15 @@ int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t e
                                         "], got [" + std::to_string(enc_len) + " " + std::to_string(enc_dim) + "]");
     if (!encs) return fail(WH_ERR_INVALID, "seq: null encoder outputs");
     WH_HIP(hipSetDevice(m->device));
+    if (dev)
+        for (int e = 0; e < (shared ? 1 : S); e++) {
+            hipPointerAttribute_t at;
+            const hipError_t pe = encs[e] ? hipPointerGetAttributes(&at, encs[e]) : hipErrorInvalidValue;
+            if (pe != hipSuccess) (void)hipGetLastError();
+            if (pe != hipSuccess || at.type != hipMemoryTypeDevice || at.device != m->device)
+                return fail(WH_ERR_INVALID, "seq: encoder output " + std::to_string(e) +
+                                                " is not device memory of the model's device");
+        }
     std::unique_ptr<wh_seq> s(new wh_seq());
     s->m = m;
     s->S = S;
@@ -699,12 +709,17 @@ int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t e
         WH_HIP(hipMemcpy(s->sb.nst, zf.data(), sizeof(float) * S, hipMemcpyHostToDevice));
     }
     // cross K/V projections of every encoder output (decoder.go:923-940), once per sequence
-    float *enc = nullptr;
-    WH_HIP(hipMalloc(&enc, sizeof(float) * (size_t)enc_len * d));
+    float *stage = nullptr;  // host encoder outputs are uploaded here one at a time
+    if (!dev) WH_HIP(hipMalloc(&stage, sizeof(float) * (size_t)enc_len * d));
     for (int e = 0; e < s->n_enc; e++) {
-        if (!encs[e]) { (void)hipFree(enc); return fail(WH_ERR_INVALID, "seq: null encoder output"); }
-        hipError_t he = hipMemcpyAsync(enc, encs[e], sizeof(float) * (size_t)enc_len * d, hipMemcpyHostToDevice, s->st);
-        if (he != hipSuccess) { (void)hipFree(enc); return fail(WH_ERR_HIP, "hip: encoder upload failed"); }
+        if (!encs[e]) { (void)hipFree(stage); return fail(WH_ERR_INVALID, "seq: null encoder output"); }
+        const float *enc = encs[e];
+        if (!dev) {
+            hipError_t he =
+                hipMemcpyAsync(stage, encs[e], sizeof(float) * (size_t)enc_len * d, hipMemcpyHostToDevice, s->st);
+            if (he != hipSuccess) { (void)hipFree(stage); return fail(WH_ERR_HIP, "hip: encoder upload failed"); }
+            enc = stage;
+        }
         for (int li = 0; li < L; li++) {
             const Layer &l = m->layers[li];
             float *K = s->crossK + ((size_t)e * L + li) * enc_len * d;
@@ -712,13 +727,13 @@ int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t e
             if ((rc = launch_cross_gemm(l.ck, enc, enc_len, nullptr, K, s->st)) ||
                 (rc = launch_cross_gemm(l.cv, enc, enc_len, l.cvb, Vv, s->st))) {
                 (void)hipStreamSynchronize(s->st);
-                (void)hipFree(enc);
+                (void)hipFree(stage);
                 return rc;
             }
         }
-        (void)hipStreamSynchronize(s->st);  // enc is reused for the next stream
+        if (!dev) (void)hipStreamSynchronize(s->st);  // the staging buffer is reused for the next stream
     }
-    (void)hipFree(enc);
+    (void)hipFree(stage);
     WH_HIP(hipStreamSynchronize(s->st));
     if ((rc = mega_setup(*s))) return rc;
     if ((rc = batch_setup(*s))) return rc;
@@ -1024,7 +1039,7 @@ int32_t last_decode_steps() { return g_decode_steps; }
 
 int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, int32_t enc_len, int32_t enc_dim,
                         const wh_decode_params *params, int32_t *out_tokens, int32_t cap, int32_t *out_lens,
-                        const volatile int32_t *cancel) {
+                        const volatile int32_t *cancel, int32_t dev) {
     int rc;
     g_decode_steps = 0;
     for (int i = 0; i < S; i++) {
@@ -1035,7 +1050,7 @@ int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, 
                                                 std::to_string(params[i].beam_size));
     }
     wh_seq *sp = nullptr;
-    if ((rc = seq_create(m, S, encs, enc_len, enc_dim, 0, &sp))) return rc;
+    if ((rc = seq_create(m, S, encs, enc_len, enc_dim, 0, &sp, dev))) return rc;
     std::unique_ptr<wh_seq, void (*)(wh_seq *)> s(sp, seq_destroy);
     std::vector<std::vector<int32_t>> toks(S);
     std::vector<int32_t> active(S, 1), maxt(S), streak(S, 0), prev(S, -1), ids(S);
@@ -1109,7 +1124,7 @@ int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, 
 // in Go's sort.Slice order, and the prune with the reference's in-place reuse of
 // the beam objects (k_beam_select). The host reads the stop words once per step.
 int decode_beam(const wh_model *m, const float *enc, int32_t enc_len, int32_t enc_dim, const wh_decode_params *p,
-                int32_t *out_tokens, int32_t cap, int32_t *out_len, const volatile int32_t *cancel) {
+                int32_t *out_tokens, int32_t cap, int32_t *out_len, const volatile int32_t *cancel, int32_t dev) {
     if (!p) return fail(WH_ERR_INVALID, "model: decode: null params");
     if (p->prompt_len < 0 || (p->prompt_len > 0 && !p->prompt)) return fail(WH_ERR_INVALID, "model: decode: invalid prompt");
     int rc;
@@ -1137,7 +1152,7 @@ int decode_beam(const wh_model *m, const float *enc, int32_t enc_len, int32_t en
     if (P == 0) return fail(WH_ERR_INVALID, "model: decode: beam search forward: model: decode: forward: no tokens in state");
     std::vector<const float *> encs(bs, enc);
     wh_seq *sp = nullptr;
-    if ((rc = seq_create(m, bs, encs.data(), enc_len, enc_dim, 1, &sp))) return rc;
+    if ((rc = seq_create(m, bs, encs.data(), enc_len, enc_dim, 1, &sp, dev))) return rc;
     std::unique_ptr<wh_seq, void (*)(wh_seq *)> s(sp, seq_destroy);
     wh_seq &q = *s;
     // a slot's history grows by at most one token per earlier slot of its step

@@ -244,6 +244,20 @@ class HIPDecoder:
             _raise(rc)
         return list(out[:n.value])
 
+    def decode_tokens_device(self, enc_ptr, enc_len, params: DecoderParams, cancel: Optional[C.c_int32] = None):
+        """decode_tokens with the encoder output [enc_len, n_state] float32 in device
+        memory of the model's device, given as an address."""
+        ps, keep = _params_struct(params)
+        cap = len(params.prompt) + max(1, int(params.beam_size)) * (self.n_ctx + 1) + 8
+        out = (C.c_int32 * cap)()
+        n = C.c_int32()
+        cptr = C.pointer(cancel) if cancel is not None else None
+        rc = lib().wh_decode_device(self._h, int(enc_ptr), int(enc_len), self.n_state, C.byref(ps), out, cap,
+                                    C.byref(n), cptr)
+        if rc != native.WH_OK:
+            _raise(rc)
+        return list(out[:n.value])
+
     @staticmethod
     def last_decode_steps():
         """Forward steps of this thread's last decode_tokens / decode / decode_batch

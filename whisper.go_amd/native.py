@@ -92,9 +92,12 @@ _SIGS = [
     ("wh_model_set_attention_mode", C.c_int, [_P, C.c_int32]),
     ("wh_decode", C.c_int, [_P, _P, C.c_int32, C.c_int32, C.POINTER(WhDecodeParams), C.POINTER(C.c_int32),
                             C.c_int32, C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
+    ("wh_decode_device", C.c_int, [_P, _P, C.c_int32, C.c_int32, C.POINTER(WhDecodeParams), C.POINTER(C.c_int32),
+                            C.c_int32, C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     ("wh_decode_batch", C.c_int, [_P, C.c_int32, C.POINTER(_P), C.c_int32, C.c_int32, C.POINTER(WhDecodeParams),
                                   C.POINTER(C.c_int32), C.c_int32, C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     ("wh_seq_create", C.c_int, [_P, C.c_int32, C.POINTER(_P), C.c_int32, C.c_int32, C.c_int32, C.POINTER(_P)]),
+    ("wh_seq_create_device", C.c_int, [_P, C.c_int32, C.POINTER(_P), C.c_int32, C.c_int32, C.c_int32, C.POINTER(_P)]),
     ("wh_seq_destroy", C.c_int, [_P]),
     ("wh_seq_set_tokens", C.c_int, [_P, C.c_int32, C.POINTER(C.c_int32), C.c_int32, C.c_int32]),
     ("wh_seq_step_greedy", C.c_int, [_P, C.POINTER(C.c_int32), C.c_float, C.c_int32, C.c_float,
