@@ -45,9 +45,10 @@ constexpr int AKS = AK + 4;  // K tile row stride (floats): 16-byte rows, 16 row
 // SDPA of one head with head size 64 on the fp32 matrix cores
 // (ml/attention.go:193-281 with the fast-exp softmax of attention.go:93-131):
 // scores = (q . k) * scale; weight = fastexp(score - row max) / row sum;
-// out = weights . V. Each wave owns 32 queries; the QW waves of a workgroup
-// share the K and V tiles of 64 keys staged in LDS (the next tile's loads in
-// flight while the current one is used).
+// out = weights . V. Each wave owns 32 queries and one of KS interleaved shares
+// of the key tiles (64 keys each); the QW x KS waves of a workgroup stage KS
+// tiles per round in LDS (the next round's loads in flight while the current one
+// is used).
 //
 // The products are formed transposed, S^T = K Q^T and O^T = V^T P^T, with
 // v_mfma_f32_32x32x2f32: its accumulator gives lane l the column l % 32 (one
@@ -59,21 +60,31 @@ constexpr int AKS = AK + 4;  // K tile row stride (floats): 16-byte rows, 16 row
 // In S^T = K Q^T, MFMA k-index 0 carries dimensions 0-31 and index 1
 // dimensions 32-63, so each lane keeps its query's half row of q in registers.
 //
-// Pass 1 finds every row's maximum of scale * score over all keys; pass 2
-// recomputes the scores, forms the fast-exp weights against that maximum,
-// accumulates weights . V and the row sums; the output is the accumulation times
-// 1 / sum. Keys past T weigh 0 (their V rows are staged as zeros), queries past T
-// are not stored. Q, K, V, out are [T, d] with head h in columns 64h..64h+63.
-template <int QW>
-__global__ __launch_bounds__(64 * QW) void k_enc_attn_mfma(const float *Q, const float *K, const float *V, int T,
-                                                           int d, float scale, float *out) {
-    constexpr int NT = 64 * QW, NL = AK * 16 / NT;  // float4 of a tile per thread
-    static_assert(AK * 16 % NT == 0, "a tile is whole float4 rounds of the workgroup");
-    __shared__ float Ks[AK][AKS];
-    __shared__ float Vs[AK][64];
+// Pass 1 finds every row's maximum of scale * score over all keys (the shares'
+// maxima combined through LDS); pass 2 recomputes the scores, forms the fast-exp
+// weights against that maximum, accumulates weights . V and the row sums; the
+// shares' sums and products are added in share order and the output is the
+// accumulation times 1 / sum. Keys past T weigh 0 (their V rows are staged as
+// zeros), queries past T are not stored. Q, K, V, out are [T, d] with head h in
+// columns 64h..64h+63.
+template <int QW, int KS>
+constexpr size_t attn_lds() {
+    return sizeof(float) * ((size_t)KS * AK * (AKS + 64) + (size_t)KS * QW * 32);
+}
+
+template <int QW, int KS>
+__global__ __launch_bounds__(64 * QW * KS) void k_enc_attn_mfma(const float *Q, const float *K, const float *V, int T,
+                                                                int d, float scale, float *out) {
+    constexpr int NT = 64 * QW * KS, NL = AK * 16 * KS / NT;  // float4 of a round's tiles per thread
+    static_assert(AK * 16 * KS % NT == 0, "a round is whole float4 rounds of the workgroup");
+    extern __shared__ float4 lds_f4[];  // attn_lds<QW, KS>() bytes
+    float(*Ks)[AK][AKS] = (float(*)[AK][AKS])lds_f4;                       // [KS][AK][AKS]
+    float(*Vs)[AK][64] = (float(*)[AK][64])((float *)lds_f4 + KS * AK * AKS);  // [KS][AK][64]
+    float(*mxs)[QW][32] = (float(*)[QW][32])((float *)lds_f4 + KS * AK * (AKS + 64));
     const int h = blockIdx.y, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int qw = wave % QW, ks = wave / QW;
     const int ql = lane & 31, half = lane >> 5;
-    const int q = blockIdx.x * 32 * QW + wave * 32 + ql;
+    const int q = blockIdx.x * 32 * QW + qw * 32 + ql;
     const size_t col = (size_t)h * 64;
     float qr[32];
     {
@@ -85,11 +96,12 @@ __global__ __launch_bounds__(64 * QW) void k_enc_attn_mfma(const float *Q, const
             qr[4 * j] = v.x; qr[4 * j + 1] = v.y; qr[4 * j + 2] = v.z; qr[4 * j + 3] = v.w;
         }
     }
-    // tile staging: float4 i of a tile is key i / 16, dimensions 4 (i % 16) ..
-    const auto load_tile = [&](const float *src, int k0, float4 (&r)[NL]) __attribute__((always_inline)) {
+    // round staging: float4 i of a round is tile i / 1024 of the round (keys
+    // r0 + 64 (i / 1024) ..), key (i % 1024) / 16, dimensions 4 (i % 16) ..
+    const auto load_round = [&](const float *src, int r0, float4 (&r)[NL]) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < NL; j++) {
-            const int i = tid + j * NT, key = k0 + (i >> 4);
+            const int i = tid + j * NT, key = r0 + (i >> 4);
             r[j] = key < T ? *(const float4 *)(src + (size_t)key * d + col + 4 * (i & 15))
                            : make_float4(0.f, 0.f, 0.f, 0.f);
         }
@@ -98,24 +110,24 @@ __global__ __launch_bounds__(64 * QW) void k_enc_attn_mfma(const float *Q, const
 #pragma unroll
         for (int j = 0; j < NL; j++) {
             const int i = tid + j * NT;
-            *(float4 *)&Ks[i >> 4][4 * (i & 15)] = r[j];
+            *(float4 *)&Ks[i >> 10][(i >> 4) & 63][4 * (i & 15)] = r[j];
         }
     };
     const auto store_v = [&](const float4 (&r)[NL]) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < NL; j++) {
             const int i = tid + j * NT;
-            *(float4 *)&Vs[i >> 4][4 * (i & 15)] = r[j];
+            *(float4 *)&Vs[i >> 10][(i >> 4) & 63][4 * (i & 15)] = r[j];
         }
     };
-    // S^T of the staged tile: s0 keys 0-31, s1 keys 32-63, this lane's query
+    // S^T of this wave's staged tile: s0 keys 0-31, s1 keys 32-63, this lane's query
     const auto scores = [&](f32x16 &s0, f32x16 &s1) __attribute__((always_inline)) {
         s0 = f32x16{};
         s1 = f32x16{};
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const float4 ka = *(const float4 *)&Ks[ql][32 * half + 4 * j];
-            const float4 kb = *(const float4 *)&Ks[32 + ql][32 * half + 4 * j];
+            const float4 ka = *(const float4 *)&Ks[ks][ql][32 * half + 4 * j];
+            const float4 kb = *(const float4 *)&Ks[ks][32 + ql][32 * half + 4 * j];
             s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.x, qr[4 * j], s0, 0, 0, 0);
             s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kb.x, qr[4 * j], s1, 0, 0, 0);
             s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.y, qr[4 * j + 1], s0, 0, 0, 0);
@@ -128,56 +140,96 @@ __global__ __launch_bounds__(64 * QW) void k_enc_attn_mfma(const float *Q, const
     };
     // key of register i within its 32-key half of the tile
     const auto rkey = [&](int i) __attribute__((always_inline)) { return 8 * (i >> 2) + 4 * half + (i & 3); };
+    constexpr int RK = AK * KS;  // keys per round
     float4 kr[NL], vr[NL];
     // pass 1: row maxima
     float mx = -INFINITY;
-    load_tile(K, 0, kr);
-    for (int k0 = 0; k0 < T; k0 += AK) {
+    load_round(K, 0, kr);
+    for (int r0 = 0; r0 < T; r0 += RK) {
         __syncthreads();
         store_k(kr);
         __syncthreads();
-        if (k0 + AK < T) load_tile(K, k0 + AK, kr);
-        f32x16 s0, s1;
-        scores(s0, s1);
+        if (r0 + RK < T) load_round(K, r0 + RK, kr);
+        const int k0 = r0 + AK * ks;
+        if (k0 < T) {
+            f32x16 s0, s1;
+            scores(s0, s1);
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            if (k0 + rkey(i) < T) mx = fmaxf(mx, s0[i] * scale);
-            if (k0 + 32 + rkey(i) < T) mx = fmaxf(mx, s1[i] * scale);
+            for (int i = 0; i < 16; i++) {
+                if (k0 + rkey(i) < T) mx = fmaxf(mx, s0[i] * scale);
+                if (k0 + 32 + rkey(i) < T) mx = fmaxf(mx, s1[i] * scale);
+            }
         }
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    if (KS > 1) {
+        if (lane < 32) mxs[ks][qw][ql] = mx;
+        __syncthreads();
+        mx = mxs[0][qw][ql];
+#pragma unroll
+        for (int k = 1; k < KS; k++) mx = fmaxf(mx, mxs[k][qw][ql]);
+    }
     // pass 2: fast-exp weights, P.V and row sums
     f32x16 o0 = {}, o1 = {};  // output dimensions 0-31 and 32-63
     float rs = 0.0f;
-    load_tile(K, 0, kr);
-    load_tile(V, 0, vr);
-    for (int k0 = 0; k0 < T; k0 += AK) {
+    load_round(K, 0, kr);
+    load_round(V, 0, vr);
+    for (int r0 = 0; r0 < T; r0 += RK) {
         __syncthreads();
         store_k(kr);
         store_v(vr);
         __syncthreads();
-        if (k0 + AK < T) {
-            load_tile(K, k0 + AK, kr);
-            load_tile(V, k0 + AK, vr);
+        if (r0 + RK < T) {
+            load_round(K, r0 + RK, kr);
+            load_round(V, r0 + RK, vr);
         }
-        f32x16 s0, s1;
-        scores(s0, s1);
+        const int k0 = r0 + AK * ks;
+        if (k0 < T) {
+            f32x16 s0, s1;
+            scores(s0, s1);
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            s0[i] = k0 + rkey(i) < T ? fast_exp(s0[i] * scale - mx) : 0.0f;
-            s1[i] = k0 + 32 + rkey(i) < T ? fast_exp(s1[i] * scale - mx) : 0.0f;
-            rs += s0[i] + s1[i];
-        }
+            for (int i = 0; i < 16; i++) {
+                s0[i] = k0 + rkey(i) < T ? fast_exp(s0[i] * scale - mx) : 0.0f;
+                s1[i] = k0 + 32 + rkey(i) < T ? fast_exp(s1[i] * scale - mx) : 0.0f;
+                rs += s0[i] + s1[i];
+            }
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float *va = Vs[rkey(i)], *vb = Vs[32 + rkey(i)];
-            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(va[ql], s0[i], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(va[32 + ql], s0[i], o1, 0, 0, 0);
-            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[ql], s1[i], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[32 + ql], s1[i], o1, 0, 0, 0);
+            for (int i = 0; i < 16; i++) {
+                const float *va = Vs[ks][rkey(i)], *vb = Vs[ks][32 + rkey(i)];
+                o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(va[ql], s0[i], o0, 0, 0, 0);
+                o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(va[32 + ql], s0[i], o1, 0, 0, 0);
+                o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[ql], s1[i], o0, 0, 0, 0);
+                o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[32 + ql], s1[i], o1, 0, 0, 0);
+            }
         }
     }
     rs += __shfl_xor(rs, 32, 64);
+    if (KS > 1) {
+        // shares 1.. post their sums and products over the K tiles; share 0 adds them in order
+        float *post = &Ks[0][0][0];  // [KS - 1][QW][64 lanes][33]
+        __syncthreads();
+        if (ks > 0) {
+            float *p = post + (((size_t)(ks - 1) * QW + qw) * 64 + lane) * 33;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                p[i] = o0[i];
+                p[16 + i] = o1[i];
+            }
+            p[32] = rs;
+        }
+        __syncthreads();
+        if (ks > 0) return;
+#pragma unroll
+        for (int k = 1; k < KS; k++) {
+            const float *p = post + (((size_t)(k - 1) * QW + qw) * 64 + lane) * 33;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                o0[i] += p[i];
+                o1[i] += p[16 + i];
+            }
+            rs += p[32];
+        }
+    }
     if (q >= T) return;
     // the row maximum's own weight is fast_exp(0) = 1, so rs >= 1 (the
     // reference's uniform-weight branch for a zero sum cannot be taken)
@@ -253,9 +305,12 @@ int launch_enc_attn(const float *Q, const float *K, const float *V, int T, int d
     const float scale = (float)(1.0 / sqrt((double)hd));
     if (hd == 64 && d % 4 == 0 && ((uintptr_t)Q & 15) == 0 && ((uintptr_t)K & 15) == 0 &&
         ((uintptr_t)V & 15) == 0 && ((uintptr_t)out & 15) == 0) {
-        constexpr int QW = 4;
-        hipLaunchKernelGGL(k_enc_attn_mfma<QW>, dim3((T + 32 * QW - 1) / (32 * QW), H), dim3(64 * QW), 0, s, Q, K, V,
-                           T, d, scale, out);
+        constexpr int QW = 4, KS = 2;  // 4 x 32 queries per workgroup, keys in 2 shares
+        constexpr size_t lds = attn_lds<QW, KS>();
+        WH_HIP(hipFuncSetAttribute((const void *)k_enc_attn_mfma<QW, KS>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)lds));
+        hipLaunchKernelGGL((k_enc_attn_mfma<QW, KS>), dim3((T + 32 * QW - 1) / (32 * QW), H), dim3(64 * QW * KS), lds,
+                           s, Q, K, V, T, d, scale, out);
     } else {
         hipLaunchKernelGGL(k_enc_attn_any, dim3(T, H), dim3(64), (size_t)T * sizeof(float), s, Q, K, V, T, d, hd,
                            scale, out);

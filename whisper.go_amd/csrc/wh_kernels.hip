@@ -1315,53 +1315,65 @@ __device__ __forceinline__ void dequant8(const MatView &m, int r, int b, int g, 
     dq8_convert<TYPE>(q, o);
 }
 
-template <int TYPE>
 // Epilogue: v = acc + bias; gelu: C = gelu(v); res: C = res + v (res may alias C).
+// BK blocks of 32 columns per K-step (one LDS stage and two barriers per step);
+// a row's last step with fewer blocks left stages zeros in their place.
+template <int TYPE, int BK>
 __global__ __launch_bounds__(256) void k_cross_gemm(MatView w, const float *E, int T, const float *bias, float *C,
                                                     int gelu, const float *res) {
-    __shared__ float Es[64][33];  // [frame][k]; the padding keeps the operand reads conflict-free
-    __shared__ float Ws[64][33];  // [row][k]
+    constexpr int KW = 32 * BK, KP = KW + 1;  // columns per step; LDS row stride (conflict-free operand reads)
+    __shared__ float Es[64][KP];  // [frame][k]
+    __shared__ float Ws[64][KP];  // [row][k]
     const int t0 = blockIdx.y * 64, r0 = blockIdx.x * 64;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wt = (wave >> 1) * 32, wr = (wave & 1) * 32;  // this wave's quarter of the tile
     const int K = w.cols;
-    const int lr = tid >> 2, lg = tid & 3;  // tile loads: row (frame) lr, elements 8 lg .. 8 lg + 7
+    const int lr = tid >> 2, lg = tid & 3;  // tile loads: row (frame) lr, elements 8 lg .. 8 lg + 7 of each block
     f32x16 acc = {};
-    // the next K tile in registers: its loads are in flight while the current tile's
-    // products run
-    float4 ex = make_float4(0.f, 0.f, 0.f, 0.f), ey = ex;
-    Raw8 wq = {};
-    auto load_tile = [&](int b) {
+    // the next K-step in registers: its loads are in flight while the current step's
+    // matrix-core products run
+    float4 ex[BK], ey[BK];
+    Raw8 wq[BK];
+    auto load_step = [&](int b0) {
         const int t = t0 + lr;
-        ex = make_float4(0.f, 0.f, 0.f, 0.f);
-        ey = ex;
-        if (t < T) {
-            const float4 *p = (const float4 *)(E + (size_t)t * K + b * 32 + 8 * lg);
-            ex = p[0];
-            ey = p[1];
+#pragma unroll
+        for (int u = 0; u < BK; u++) {
+            const int b = b0 + u;
+            ex[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            ey[u] = ex[u];
+            wq[u] = {};
+            if (b < w.nb) {
+                if (t < T) {
+                    const float4 *p = (const float4 *)(E + (size_t)t * K + b * 32 + 8 * lg);
+                    ex[u] = p[0];
+                    ey[u] = p[1];
+                }
+                if (r0 + lr < w.rows) dq8_load<TYPE>(w, r0 + lr, b, lg, wq[u]);
+            }
         }
-        if (r0 + lr < w.rows) dq8_load<TYPE>(w, r0 + lr, b, lg, wq);
     };
-    load_tile(0);
-    for (int b = 0; b < w.nb; b++) {
-        {
-            float *e = &Es[lr][8 * lg];
-            e[0] = ex.x; e[1] = ex.y; e[2] = ex.z; e[3] = ex.w; e[4] = ey.x; e[5] = ey.y; e[6] = ey.z; e[7] = ey.w;
+    load_step(0);
+    for (int b0 = 0; b0 < w.nb; b0 += BK) {
+#pragma unroll
+        for (int u = 0; u < BK; u++) {
+            float *e = &Es[lr][32 * u + 8 * lg];
+            e[0] = ex[u].x; e[1] = ex[u].y; e[2] = ex[u].z; e[3] = ex[u].w;
+            e[4] = ey[u].x; e[5] = ey[u].y; e[6] = ey[u].z; e[7] = ey[u].w;
             float o[8];
-            if (r0 + lr < w.rows) {
-                dq8_convert<TYPE>(wq, o);
+            if (r0 + lr < w.rows && b0 + u < w.nb) {
+                dq8_convert<TYPE>(wq[u], o);
             } else {
 #pragma unroll
                 for (int j = 0; j < 8; j++) o[j] = 0.0f;
             }
 #pragma unroll
-            for (int j = 0; j < 8; j++) Ws[lr][8 * lg + j] = o[j];
+            for (int j = 0; j < 8; j++) Ws[lr][32 * u + 8 * lg + j] = o[j];
         }
         __syncthreads();
-        if (b + 1 < w.nb) load_tile(b + 1);
+        if (b0 + BK < w.nb) load_step(b0 + BK);
         // A (32 frames x 2 k): lane -> frame lane % 32, k lane / 32; B (2 k x 32 rows) likewise
 #pragma unroll
-        for (int kk = 0; kk < 32; kk += 2) {
+        for (int kk = 0; kk < KW; kk += 2) {
             const float av = Es[wt + (lane & 31)][kk + (lane >> 5)];
             const float bv = Ws[wr + (lane & 31)][kk + (lane >> 5)];
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
@@ -1457,12 +1469,12 @@ int launch_cross_gemm(const DevMat &w, const float *enc, int enc_len, const floa
         return WH_OK;
     }
     switch (w.type) {
-    case 0: hipLaunchKernelGGL(k_cross_gemm<0>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
-    case 2: hipLaunchKernelGGL(k_cross_gemm<2>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
-    case 3: hipLaunchKernelGGL(k_cross_gemm<3>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
-    case 6: hipLaunchKernelGGL(k_cross_gemm<6>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
-    case 7: hipLaunchKernelGGL(k_cross_gemm<7>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
-    case 8: hipLaunchKernelGGL(k_cross_gemm<8>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
+    case 0: hipLaunchKernelGGL((k_cross_gemm<0, 2>), grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
+    case 2: hipLaunchKernelGGL((k_cross_gemm<2, 2>), grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
+    case 3: hipLaunchKernelGGL((k_cross_gemm<3, 2>), grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
+    case 6: hipLaunchKernelGGL((k_cross_gemm<6, 2>), grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
+    case 7: hipLaunchKernelGGL((k_cross_gemm<7, 2>), grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
+    case 8: hipLaunchKernelGGL((k_cross_gemm<8, 2>), grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
     default: return fail(WH_ERR_UNSUPPORTED, "cross gemm: unsupported type");
     }
     WH_HIP(hipGetLastError());
