@@ -44,6 +44,7 @@ struct BArgs {
     unsigned *flags;                      // [grid] last published phase
     unsigned *err;                        // set when a wait gives up
     float scale;                          // 1/sqrt(64)
+    int mfma;                             // GEMV rows on the matrix cores
 };
 
 constexpr int LMAX = 32;              // layers at most

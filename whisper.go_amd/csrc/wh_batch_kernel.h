@@ -555,15 +555,178 @@ __device__ __forceinline__ void finish(int P, int nr, int row1, int S, unsigned 
     }
 }
 
+// ---- GEMV on the matrix cores ---------------------------------------------------------
+// 16 weight rows x up to 16 states per tile with v_mfma_f32_16x16x4f32 (fp32
+// operands: the codes are exact small integers). Lane l (r = l % 16, kq = l / 16)
+// supplies, for the block's j-th product, element 8 kq + j of state r's staged
+// row (chunks 2 kq and 2 kq + 1 of the block, two LDS reads) and of weight row r
+// (its code: Q8_0 byte 8 kq + j; 4/5-bit nibble j of the word of bytes 4 kq ..,
+// the nibbles interleaved in the device layout, plus high bit 8 kq + j); D register
+// i of lane l is state 4 kq + i, row r, scaled per block (d, and the offset or m
+// through the staged block sums) into the total. Each staged value is read by one
+// lane per block instead of one per row, the lanes' dot products become 8 matrix
+// instructions. The waves take the blocks of a tile in turn; their tiles are summed
+// in wave order through LDS and thread t < 256 runs the epilogue of state t / 16,
+// row t % 16.
+struct MBlk {
+    uint32_t a, b;  // the lane's code bytes (Q8_0: 8 in a, b; 4/5-bit: 4 in a)
+    uint32_t s, h;  // scale word(s), Q5 high bits
+};
+
+template <int TYPE>
+__device__ __forceinline__ void mblk_load(const MatView &m, int row, int b, int kq, MBlk &k) {
+    const size_t blk = (size_t)row * m.nb + b;
+    if constexpr (TYPE == 8) {
+        k.a = *(gcu32 *)(m.qs + blk * 32 + 8 * kq);
+        k.b = *(gcu32 *)(m.qs + blk * 32 + 8 * kq + 4);
+        k.s = ((gcu16 *)m.sc)[blk];
+        k.h = 0u;
+    } else {
+        k.a = *(gcu32 *)(m.qs + blk * 16 + 4 * kq);
+        k.b = 0u;
+        if constexpr (TYPE == 3 || TYPE == 7) k.s = ((gcu32 *)m.sc)[blk];
+        else k.s = ((gcu16 *)m.sc)[blk];
+        if constexpr (TYPE == 6 || TYPE == 7) k.h = ((gcu32 *)m.qh)[blk];
+        else k.h = 0u;
+    }
+}
+
+// code of element 8 kq + j of the lane's block
+template <int TYPE>
+__device__ __forceinline__ float mcode(const MBlk &k, int kq, int j) {
+    if constexpr (TYPE == 8) {
+        const uint32_t w = j < 4 ? k.a : k.b;
+        return (float)(int)__builtin_amdgcn_sbfe((int)w, 8 * (j & 3), 8);  // the builtin's type is unsigned
+    } else {
+        uint32_t c = (k.a >> (4 * j)) & 0xFu;
+        if constexpr (TYPE == 6 || TYPE == 7) c |= ((k.h >> (8 * kq + j)) & 1u) << 4;
+        return (float)c;
+    }
+}
+
+// staged block b (of nbc) against the lane's codes k; adds the block's terms to acc
+template <int TYPE>
+__device__ __forceinline__ void mdot(const MBlk &k, int S, int nbc, int b, const Lds &L, f32x4 &acc) {
+    const int lane = threadIdx.x & 63, lr = lane & 15, kq = lane >> 4;
+    float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
+    if (lr < S) {
+        x0 = L.xs[slot(lr, nbc, b, 2 * kq)];
+        x1 = L.xs[slot(lr, nbc, b, 2 * kq + 1)];
+    }
+    const float xa[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 8; j++) t = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[j], mcode<TYPE>(k, kq, j), t, 0, 0, 0);
+    Blk sb;
+    sb.s = k.s;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int st = 4 * kq + i;
+        const float sxv = (TYPE != 8 && st < S) ? L.sx[st * nbc + b] : 0.0f;
+        acc[i] += bscale<TYPE>(sb, t[i], sxv);
+    }
+}
+
+// The waves' tiles summed in wave order (in the LayerNorm weight area, free once
+// the inputs are staged); out[t] for t < 256 is state t / 16, row t % 16.
+__device__ __forceinline__ void mreduce(const f32x4 &acc, const Lds &L) {
+    const int lane = threadIdx.x & 63, wv = wave_id(), lr = lane & 15, kq = lane >> 4;
+    f32x4 *red = (f32x4 *)L.lw;  // [NWV][64]
+    red[wv * 64 + lane] = acc;
+    __syncthreads();
+    if (wv == 0) {
+        f32x4 sum = red[lane];
+#pragma unroll
+        for (int w = 1; w < NWV; w++) sum += red[w * 64 + lane];
+#pragma unroll
+        for (int i = 0; i < 4; i++) L.red[(4 * kq + i) * 16 + lr] = sum[i];
+    }
+    __syncthreads();
+}
+
+template <int TYPE, class Stage, class Pre, class Epi>
+__device__ __forceinline__ void gemv_mf(const MatView &w, int row0, int row1, int S, unsigned amask, Stage stage,
+                                        const Lds &L, Pre pre, Epi epi) {
+    constexpr int U = 4;  // blocks of a wave per group
+    const int nb = w.nb, lane = threadIdx.x & 63, wv = wave_id(), lr = lane & 15, kq = lane >> 4;
+    const int ntile = (row1 - row0 + 15) / 16;
+    const int ng = ((nb + NWV - 1) / NWV + U - 1) / U;  // groups of a tile (the same for every wave)
+    const int NUn = ntile * ng;
+    const int et = threadIdx.x, es = et >> 4, er = et & 15;  // epilogue: state es, row er of a tile
+    decltype(pre(0, 0)) ep;
+    const auto load_ep = [&](int tile) __attribute__((always_inline)) {
+        if (et < 256) ep = pre(min(es, S - 1), min(row0 + 16 * tile + er, row1 - 1));
+    };
+    const auto load_unit = [&](int u, MBlk (&k)[U]) __attribute__((always_inline)) {
+        const int tile = u / ng, g = u - tile * ng;
+        const int row = min(row0 + 16 * tile + lr, row1 - 1);
+#pragma unroll
+        for (int v = 0; v < U; v++) mblk_load<TYPE>(w, row, min(wv + NWV * (g * U + v), nb - 1), kq, k[v]);
+    };
+    MBlk cur[U], nxt[U];
+    load_unit(0, cur);
+    load_ep(0);
+    stage();
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < NUn; u++) {
+        const int tile = u / ng, g = u - tile * ng;
+        if (u + 1 < NUn) load_unit(u + 1, nxt);
+#pragma unroll
+        for (int v = 0; v < U; v++) {
+            const int b = wv + NWV * (g * U + v);
+            if (b < nb) mdot<TYPE>(cur[v], S, nb, b, L, acc);
+        }
+#pragma unroll
+        for (int v = 0; v < U; v++) cur[v] = nxt[v];
+        if (g == ng - 1) {
+            mreduce(acc, L);
+            const int row = row0 + 16 * tile + er;
+            if (et < 256 && es < S && row < row1 && ((amask >> es) & 1u)) epi(es, row, L.red[et], ep);
+            if (tile + 1 < ntile) load_ep(tile + 1);
+            acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    __syncthreads();
+}
+
+template <int TYPE, class FillC, class Pre, class Epi>
+__device__ __forceinline__ void gemv_cols_mf(const MatView &w, int row0, int row1, int S, unsigned amask, FillC fillc,
+                                             const Lds &L, Pre pre, Epi epi) {
+    // one tile: the host sizes the grid so a workgroup has at most 16 rows here
+    const int nb = w.nb, per = XBLK / S, lane = threadIdx.x & 63, wv = wave_id(), lr = lane & 15, kq = lane >> 4;
+    const int et = threadIdx.x, es = et >> 4, er = et & 15;
+    const int row = min(row0 + lr, row1 - 1);
+    decltype(pre(0, 0)) ep;
+    if (et < 256) ep = pre(min(es, S - 1), min(row0 + er, row1 - 1));
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < nb; c0 += per) {
+        const int nbc = min(per, nb - c0);
+        stage_cols(S, nbc, [&]() __attribute__((always_inline)) { fillc(c0, nbc); }, L.xs, L.sx, TYPE != 8);
+        for (int b = wv; b < nbc; b += NWV) {
+            MBlk k;
+            mblk_load<TYPE>(w, row, c0 + b, kq, k);
+            mdot<TYPE>(k, S, nbc, b, L, acc);
+        }
+        __syncthreads();
+    }
+    mreduce(acc, L);
+    if (et < 256 && es < S && row0 + er < row1 && ((amask >> es) & 1u)) epi(es, row0 + er, L.red[et], ep);
+    __syncthreads();
+}
+
 // Rows [row0, row1) of w against inputs that stage() puts in LDS (all columns).
 // A workgroup without rows returns at once (uniformly). The work is a sequence
 // of units (row pass, block step); the first two units' weight blocks and the
 // first pass's epilogue operands are loaded before stage() runs, and every unit
 // loads the blocks of the unit two ahead while it computes.
-template <int TYPE, int G, class Stage, class Pre, class Epi>
+template <int TYPE, int G, bool MF, class Stage, class Pre, class Epi>
 __device__ __forceinline__ void gemv(const MatView &w, int row0, int row1, int S, unsigned amask, Stage stage,
                                      const Lds &L, Pre pre, Epi epi) {
     if (row0 >= row1) return;
+    if constexpr (MF) {
+        gemv_mf<TYPE>(w, row0, row1, S, amask, stage, L, pre, epi);
+        return;
+    }
     constexpr int PR = NWV * RW * (64 / G);  // rows of a workgroup's pass
     const int nb = w.nb, gl = (int)(threadIdx.x & 63) % G;
     const int NBJ = (nb + G - 1) / G, NU = (row1 - row0 + PR - 1) / PR * NBJ;
@@ -604,10 +767,14 @@ __device__ __forceinline__ void gemv(const MatView &w, int row0, int row1, int S
 // over the columns, staged by fillc(c0, nbc); each wave keeps its rows' sums
 // across the passes (the host sizes the grid so a workgroup has at most one pass
 // of rows).
-template <int TYPE, int G, class FillC, class Pre, class Epi>
+template <int TYPE, int G, bool MF, class FillC, class Pre, class Epi>
 __device__ __forceinline__ void gemv_cols(const MatView &w, int row0, int row1, int S, unsigned amask, FillC fillc,
                                           const Lds &L, Pre pre, Epi epi) {
     if (row0 >= row1) return;
+    if constexpr (MF) {
+        gemv_cols_mf<TYPE>(w, row0, row1, S, amask, fillc, L, pre, epi);
+        return;
+    }
     const int nb = w.nb, per = XBLK / S, gl = (int)(threadIdx.x & 63) % G;
     const int nr = pslots<G>(row0, row1);
     decltype(pre(0, 0)) ad[RW];
@@ -633,18 +800,18 @@ __device__ __forceinline__ void gemv_cols(const MatView &w, int row0, int row1, 
 }
 
 // All columns staged by fillc when they fit, else column passes.
-template <int TYPE, int G, class FillC, class Pre, class Epi>
+template <int TYPE, int G, bool MF, class FillC, class Pre, class Epi>
 __device__ __forceinline__ void gemv_src(const MatView &w, int row0, int row1, int S, unsigned amask, FillC fillc,
                                          const Lds &L, Pre pre, Epi epi) {
     if (w.nb <= XBLK / S)
-        gemv<TYPE, G>(
+        gemv<TYPE, G, MF>(
             w, row0, row1, S, amask,
             [&]() __attribute__((always_inline)) {
                 stage_cols(S, w.nb, [&]() __attribute__((always_inline)) { fillc(0, w.nb); }, L.xs, L.sx, TYPE != 8);
             },
             L, pre, epi);
     else
-        gemv_cols<TYPE, G>(w, row0, row1, S, amask, fillc, L, pre, epi);
+        gemv_cols<TYPE, G, MF>(w, row0, row1, S, amask, fillc, L, pre, epi);
 }
 
 __device__ __forceinline__ int split(int n, int w, int W) { return (int)((long)n * w / W); }
@@ -660,8 +827,9 @@ struct PreX2 {  // x2 of the row, the bias
     float b;
 };
 
-// G: lanes per row group, 32 for models of width <= 1024, else 64
-template <int TYPE, int G>
+// G: lanes per row group, 32 for models of width <= 1024, else 64; MF: GEMV rows on
+// the matrix cores (gemv_mf) instead of the lanes' dot products
+template <int TYPE, int G, bool MF>
 __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
     extern __shared__ float4 lds4[];
     Lds L;
@@ -710,7 +878,7 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
     const auto sa_rows = [&](const BLayer *ly, uint64_t *sal, int r0, int r1, unsigned t) __attribute__((always_inline)) {
         const float *vp = ly->kv + plane;
         const float *sob = ly->sob;
-        gemv_src<TYPE, G>(
+        gemv_src<TYPE, G, MF>(
             ly->so, r0, r1, S, amask,
             [&](int c0, int nbc) __attribute__((always_inline)) {
                 burst(S, d, c0, nbc,
@@ -726,7 +894,7 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
         const float *lw = ly->ln1w, *lb = ly->ln1b;
         float *kv = ly->kv;
         const float *svb = ly->svb;
-        gemv<TYPE, G>(ly->sqkv, d + r0, d + r1, S, amask,
+        gemv<TYPE, G, MF>(ly->sqkv, d + r0, d + r1, S, amask,
                    [&]() __attribute__((always_inline)) {
                        stage_ln(S, d,
                                 [&]() __attribute__((always_inline)) {
@@ -747,7 +915,7 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
                              unsigned t) __attribute__((always_inline)) {
         const float *lw = ly->ln2w, *lb = ly->ln2b;
         const float *cqb = ly->cqb;
-        gemv<TYPE, G>(ly->cq, r0, r1, S, amask,
+        gemv<TYPE, G, MF>(ly->cq, r0, r1, S, amask,
                    [&]() __attribute__((always_inline)) {
                        stage_ln(S, d,
                                 [&]() __attribute__((always_inline)) {
@@ -959,7 +1127,7 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
         const unsigned tF = ++g;
         {
             const float *cob = ly->cob;
-            gemv_src<TYPE, G>(
+            gemv_src<TYPE, G, MF>(
                 ly->co, split(d, w, W), split(d, w + 1, W), S, amask, fill_pairs(atg, tX, d, d), L,
                 [=](int s, int r) {
                     return PreXS{ldp(xg + (size_t)s * d + r), ldp(sal + (size_t)s * d + r), ldg(cob + r)};
@@ -976,7 +1144,7 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
             const int r0 = split(4 * d, w, W), r1 = split(4 * d, w + 1, W);
             if (r0 < r1) {
                 const float *fc1b = ly->fc1b, *lw = ly->ln3w, *lb = ly->ln3b;
-                gemv<TYPE, G>(ly->fc1, r0, r1, S, amask,
+                gemv<TYPE, G, MF>(ly->fc1, r0, r1, S, amask,
                            [&]() __attribute__((always_inline)) {
                                stage_ln(S, d,
                                         [&]() __attribute__((always_inline)) {
@@ -995,7 +1163,7 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
         const unsigned tH = ++g;
         {
             const float *fc2b = ly->fc2b;
-            gemv_src<TYPE, G>(
+            gemv_src<TYPE, G, MF>(
                 ly->fc2, split(d, w, W), split(d, w + 1, W), S, amask, fill_pairs(hg, tG, (size_t)4 * d, 4 * d), L,
                 [=](int s, int r) { return PreX2{ldp(x2g + (size_t)s * d + r), ldg(fc2b + r)}; },
                 [=](int s, int r, float v, PreX2 p) {
@@ -1011,7 +1179,7 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
             const float *lw = a.lnw, *lb = a.lnb;
             float *lg = a.logits;
             const int V = a.V;
-            gemv<TYPE, G>(a.tok, r0, r1, S, amask,
+            gemv<TYPE, G, MF>(a.tok, r0, r1, S, amask,
                        [&]() __attribute__((always_inline)) {
                            stage_ln(S, d,
                                     [&]() __attribute__((always_inline)) {
@@ -1031,7 +1199,8 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
 template <int TYPE>
 int launch_type(int grid, const BArgs &a, hipStream_t st) {
     void *args[] = {(void *)&a};
-    const void *fn = a.d <= 1024 ? (const void *)k_fwd_batch<TYPE, 32> : (const void *)k_fwd_batch<TYPE, 64>;
+    const void *fn = a.mfma ? (a.d <= 1024 ? (const void *)k_fwd_batch<TYPE, 32, true> : (const void *)k_fwd_batch<TYPE, 64, true>)
+                            : (a.d <= 1024 ? (const void *)k_fwd_batch<TYPE, 32, false> : (const void *)k_fwd_batch<TYPE, 64, false>);
     WH_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BYTES));
     WH_HIP(hipLaunchCooperativeKernel(fn, dim3(grid), dim3(NT), args, LDS_BYTES, st));
     return WH_OK;

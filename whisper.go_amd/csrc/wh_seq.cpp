@@ -503,6 +503,13 @@ int batch_setup(wh_seq &s) {
     WH_HIP(hipMemsetAsync(a.flags, 0, sizeof(unsigned) * W, s.st));
     WH_HIP(hipMemsetAsync(a.err, 0, sizeof(unsigned), s.st));
     a.scale = (float)(1.0 / sqrt(64.0));
+    // GEMV rows on the matrix cores from 9 states (measured: 16 large-v3 Q4_1 streams
+    // 2292 against 2172 tokens/s; beam 5 small Q5_1 1047 against 1305 steps/s);
+    // WHISPER_HIP_BATCH_MFMA = 0 or 1 forces the choice
+    {
+        const int mf = env_int("WHISPER_HIP_BATCH_MFMA", -1);
+        a.mfma = mf < 0 ? s.S >= 9 : mf != 0;
+    }
     WH_HIP(hipHostMalloc((void **)&s.batch_errp, sizeof(unsigned), hipHostMallocDefault));
     *s.batch_errp = 0;
     WH_HIP(hipStreamSynchronize(s.st));
