@@ -81,6 +81,7 @@ def cpu_baseline(wh, tensors, meta, enc, prompt, n_tokens, gpu_tokens):
     st.prepare_cross(enc)  # the one-time cross K/V precompute, multi-threaded, untimed
     t_cross = time.time() - t0
     toks = list(prompt)
+    margins = []
     t1 = time.perf_counter()
     for _ in range(n_tokens):
         logits = st.forward(enc)
@@ -88,6 +89,8 @@ def cpu_baseline(wh, tensors, meta, enc, prompt, n_tokens, gpu_tokens):
         nxt = orc.sample_greedy(cur, 1.0, eot=50256)
         toks.append(int(nxt))
         st.push(nxt)
+        top2 = np.partition(cur, -2)[-2:]
+        margins.append(float(abs(top2[1] - top2[0]) / max(float(np.max(np.abs(cur))), 1e-30)))
     dt = time.perf_counter() - t1
     gen = toks[len(prompt):]
     match, n = prefix_match(gen, gpu_tokens)
@@ -97,7 +100,11 @@ def cpu_baseline(wh, tensors, meta, enc, prompt, n_tokens, gpu_tokens):
             "sample": f"{n_tokens} greedy steps of the same workload after the cross K/V precompute "
                       f"({t_cross:.1f}s on {threads} threads, untimed); the batch-1 GEMV is single-threaded "
                       f"as in the reference",
-            "tokens_match_gpu": match, "tokens_compared": n}
+            "tokens_match_gpu": match, "tokens_compared": n,
+            "min_top1_top2_margin": round(min(margins), 6) if margins else None,
+            "fragile_steps": sum(m < 1e-5 for m in margins),
+            "margin_note": "(top-1 - top-2) / max |logit| of each sampled step's penalised logits; a step is "
+                           "fragile below 1e-5, where fp32 reassociation could flip the argmax"}
 
 
 def generate_n(seq, n):
@@ -161,14 +168,21 @@ def run_decode(args):
     dec = wh.HIPDecoder(tensors, meta, device=0)
     if dec.weight_bytes != wbytes:
         raise SystemExit(f"bench: device weight bytes {dec.weight_bytes} != {wbytes}")
+    log(f"bench: weights uploaded in {time.time() - t0:.2f}s")
+    # first token from the host encoder output: sequence creation (encoder output
+    # upload + the cross K/V of every layer) and the first step
+    t1 = time.perf_counter()
     seq = dec.sequence([enc])
     seq.set_tokens(0, prompt)
+    setup_ms = (time.perf_counter() - t1) * 1e3
     persistent = seq.persistent[0]
-    log(f"bench: uploaded + cross K/V in {time.time() - t0:.2f}s, persistent kernel: {persistent}")
+    log(f"bench: cross K/V in {setup_ms:.1f} ms, persistent kernel: {persistent}")
     t1 = time.perf_counter()
     tokens = generate_n(seq, 1)
     first_ms = (time.perf_counter() - t1) * 1e3
+    t1 = time.perf_counter()
     tokens += generate_n(seq, args.warmup - 1) if args.warmup > 1 else []
+    t_warm_ms = (time.perf_counter() - t1) * 1e3
     # timed region: HIP events around each launch give the kernel's own time
     seq.set_profiling(True)
     launches0 = seq.persistent[1]
@@ -199,6 +213,9 @@ def run_decode(args):
                    "prompt": prompt, "steps_timed": args.steps, "weights": args.qtype},
         "path": "persistent" if persistent else "multi-kernel",
         "first_token_ms": round(first_ms, 3),
+        "sequence_setup_ms": round(setup_ms, 3),
+        "first_token_with_cross_kv_ms": round(setup_ms + first_ms, 3),
+        "end_to_end_ms": round(setup_ms + first_ms + (t_warm_ms + dt * 1e3), 3),
         "weight_bytes_per_token": wbytes,
         "weight_roofline_frac": round(wbytes * value / (HBM_PEAK_GBS * 1e9), 4),
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
