@@ -209,23 +209,40 @@ def test_reference_test_fixture(wh, orc, gpu):
     assert dec.decode_tokens(enc, p) == ref.decode(enc, p)
 
 
-def test_textbook_attention_mode_runs(wh, orc, gpu):
-    """Opt-in mode 1 (textbook causal mask over the cache) against a numpy
-    restatement of the same forward for the first steps."""
+def test_textbook_attention_mode_vs_numpy(wh, orc, gpu):
+    """Opt-in mode 1 (textbook causal mask over the KV cache) against the float64
+    numpy restatement of the same forward with the oracle's fast-exp softmax,
+    for five greedy steps from position 0. The restatement is pinned on the CPU
+    against a whole-block forward through the oracle's causal SDPA. At position 0
+    both modes see one key, so the first step equals the reference mode exactly;
+    from position 1 the reference mode is far from the textbook logits."""
+    from test_oracle_decoder import NumpyDecoder
+
     tensors, meta = _model(wh, "mode1", 8, (800, 128, 2, 1, 32))
     enc = wh.synth.encoder_output("mode1", 128, enc_len=40)
     dec = wh.HIPDecoder(tensors, meta)
     dec.set_attention_mode(1)
     seq = dec.sequence([enc])
     seq.set_tokens(0, [1])
-    ids0, l0 = seq.step_greedy(logits=True)
-    ids1, l1 = seq.step_greedy(logits=True)
-    assert np.all(np.isfinite(l0)) and np.all(np.isfinite(l1))
+    npd = NumpyDecoder(orc, tensors, meta, causal=True, fast=True)
+    ref = NumpyDecoder(orc, tensors, meta, fast=True)
+    toks = [1]
+    for step in range(5):
+        ids, lg = seq.step_greedy(logits=True)
+        want = npd.forward(toks, enc)
+        ref_mode = ref.forward(toks, enc)
+        assert rel_err(lg[0], want) < 1e-4, (step, rel_err(lg[0], want))
+        if step > 0:
+            assert rel_err(ref_mode, want) > 1e-2, step
+        toks.append(int(ids[0]))
     # at position 0 both modes see one key: logits equal the reference mode
     dec2 = wh.HIPDecoder(tensors, meta)
     s2 = dec2.sequence([enc])
     s2.set_tokens(0, [1])
     _, m0 = s2.step_greedy(logits=True)
+    s1 = dec.sequence([enc])
+    s1.set_tokens(0, [1])
+    _, l0 = s1.step_greedy(logits=True)
     assert rel_err(l0[0], m0[0]) < 1e-6
 
 

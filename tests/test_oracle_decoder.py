@@ -24,47 +24,85 @@ class NumpyDecoder:
     """decoder.go restated in float64 with exact softmax. Self-attention
     follows P1/P2: only KV-cache row 0 is attended (it holds k,v only when
     the forward ran at position 0). Cross-attention follows P3: head h, key t
-    reads row h*(T/H) + t//H, columns (t%H)*hd ... +hd of the [T, d] projection."""
+    reads row h*(T/H) + t//H, columns (t%H)*hd ... +hd of the [T, d] projection.
 
-    def __init__(self, orc, tensors, meta):
+    causal=True is the library's opt-in textbook mode instead: every forward
+    appends its k, v to the cache and head h attends to all cached rows
+    0..pos (an ordinary causal decoder step). fast=True runs both softmaxes
+    through the oracle's fast-exp softmax (attention.go:93-131) in float32,
+    as the device does; everything else stays float64."""
+
+    def __init__(self, orc, tensors, meta, causal=False, fast=False):
+        self.orc = orc
         self.W = {t.name: _deq(orc, t) for t in tensors}
         self.H, self.L, self.d = meta["n_head"], meta["n_layer"], meta["n_state"]
+        self.causal, self.fast = causal, fast
         self.row0_v = None
+        self.cache = None
+
+    def _softmax(self, s):
+        if self.fast:
+            return self.orc.softmax(s.astype(np.float32), fast=True).astype(np.float64)
+        pr = np.exp(s - s.max())
+        return pr / pr.sum()
+
+    def _self_attn(self, i, pos, xl):
+        W, H, d = self.W, self.H, self.d
+        p = f"decoder.blocks.{i}."
+        v = W[p + "self_attn.value.weight"] @ xl + W[p + "self_attn.value.bias"]
+        if not self.causal:
+            if pos == 0:
+                self.row0_v[i] = v
+            return self.row0_v[i] if self.row0_v is not None and self.row0_v[i] is not None else np.zeros(d)
+        hd = d // H
+        q = W[p + "self_attn.query.weight"] @ xl + W[p + "self_attn.query.bias"]
+        k = W[p + "self_attn.key.weight"] @ xl
+        K, V = self.cache[i]
+        K[pos], V[pos] = k, v
+        out = np.zeros(d)
+        for h in range(H):
+            sl = slice(h * hd, (h + 1) * hd)
+            pr = self._softmax(K[:pos + 1, sl] @ q[sl] / math.sqrt(hd))
+            out[sl] = pr @ V[:pos + 1, sl]
+        return out
+
+    def _cross_attn(self, i, xl, enc):
+        W, H, d = self.W, self.H, self.d
+        hd, T = d // H, enc.shape[0]
+        p = f"decoder.blocks.{i}."
+        q = W[p + "cross_attn.query.weight"] @ xl + W[p + "cross_attn.query.bias"]
+        K = enc @ W[p + "cross_attn.key.weight"].T
+        V = enc @ W[p + "cross_attn.value.weight"].T + W[p + "cross_attn.value.bias"]
+        out = np.zeros(d)
+        for h in range(H):
+            rows = h * (T // H) + np.arange(T) // H
+            cols = (np.arange(T) % H)[:, None] * hd + np.arange(hd)[None, :]
+            Kh, Vh = K[rows[:, None], cols], V[rows[:, None], cols]
+            pr = self._softmax(Kh @ q[h * hd:(h + 1) * hd] / math.sqrt(hd))
+            out[h * hd:(h + 1) * hd] = pr @ Vh
+        return W[p + "cross_attn.out.weight"] @ out + W[p + "cross_attn.out.bias"]
+
+    def _mlp(self, i, x):
+        W, p = self.W, f"decoder.blocks.{i}."
+        xl = _ln(x, W[p + "mlp_ln.weight"], W[p + "mlp_ln.bias"])
+        return W[p + "mlp.2.weight"] @ _gelu(W[p + "mlp.0.weight"] @ xl + W[p + "mlp.0.bias"]) + W[p + "mlp.2.bias"]
 
     def forward(self, tokens, enc):
-        W, H, d = self.W, self.H, self.d
-        hd = d // H
+        W, d = self.W, self.d
         pos = len(tokens) - 1
         x = W["decoder.token_embedding.weight"][tokens[-1]] + W["decoder.positional_embedding"][pos]
         enc = enc.astype(np.float64)
-        T = enc.shape[0]
-        if pos == 0:
+        if pos == 0 or self.cache is None:
             self.row0_v = [None] * self.L
+            n_ctx = W["decoder.positional_embedding"].shape[0]
+            self.cache = [(np.zeros((n_ctx, d)), np.zeros((n_ctx, d))) for _ in range(self.L)]
         for i in range(self.L):
             p = f"decoder.blocks.{i}."
             xl = _ln(x, W[p + "self_attn_ln.weight"], W[p + "self_attn_ln.bias"])
-            v = W[p + "self_attn.value.weight"] @ xl + W[p + "self_attn.value.bias"]
-            if pos == 0:
-                self.row0_v[i] = v
-            attn = self.row0_v[i] if self.row0_v is not None and self.row0_v[i] is not None else np.zeros(d)
+            attn = self._self_attn(i, pos, xl)
             x = x + (W[p + "self_attn.out.weight"] @ attn + W[p + "self_attn.out.bias"])
-            xl = _ln(x, W[p + "cross_attn_ln.weight"], W[p + "cross_attn_ln.bias"])
-            q = W[p + "cross_attn.query.weight"] @ xl + W[p + "cross_attn.query.bias"]
-            K = enc @ W[p + "cross_attn.key.weight"].T
-            V = enc @ W[p + "cross_attn.value.weight"].T + W[p + "cross_attn.value.bias"]
-            out = np.zeros(d)
-            for h in range(H):
-                rows = h * (T // H) + np.arange(T) // H
-                cols = (np.arange(T) % H)[:, None] * hd + np.arange(hd)[None, :]
-                Kh, Vh = K[rows[:, None], cols], V[rows[:, None], cols]
-                s = Kh @ q[h * hd:(h + 1) * hd] / math.sqrt(hd)
-                pr = np.exp(s - s.max())
-                pr /= pr.sum()
-                out[h * hd:(h + 1) * hd] = pr @ Vh
-            x = x + (W[p + "cross_attn.out.weight"] @ out + W[p + "cross_attn.out.bias"])
-            xl = _ln(x, W[p + "mlp_ln.weight"], W[p + "mlp_ln.bias"])
-            hmid = _gelu(W[p + "mlp.0.weight"] @ xl + W[p + "mlp.0.bias"])
-            x = x + (W[p + "mlp.2.weight"] @ hmid + W[p + "mlp.2.bias"])
+            x = x + self._cross_attn(i, _ln(x, W[p + "cross_attn_ln.weight"], W[p + "cross_attn_ln.bias"]), enc)
+            x = x + self._mlp(i, x)
         x = _ln(x, W["decoder.ln.weight"], W["decoder.ln.bias"])
         return W["decoder.token_embedding.weight"] @ x
 
@@ -87,6 +125,55 @@ def test_forward_matches_numpy_restatement(wh, orc, qtype, prompt):
         nxt = int(np.argmax(got))
         st.push(nxt)
         toks.append(nxt)
+
+
+def _block_logits(npd, orc, tokens, enc):
+    """The textbook decoder over the whole token block at positions 0..n-1 at
+    once: self-attention is the oracle's SDPA with its causal mask j > i
+    (attention.go:250-256), which over a block starting at position 0 is the
+    ordinary causal mask. Returns the logits of every row."""
+    W, H, d = npd.W, npd.H, npd.d
+    hd, n = d // H, len(tokens)
+    enc = enc.astype(np.float64)
+    X = W["decoder.token_embedding.weight"][tokens] + W["decoder.positional_embedding"][:n]
+
+    def heads(m):
+        return m.reshape(n, H, hd).transpose(1, 0, 2)
+
+    for i in range(npd.L):
+        p = f"decoder.blocks.{i}."
+        XL = np.stack([_ln(x, W[p + "self_attn_ln.weight"], W[p + "self_attn_ln.bias"]) for x in X])
+        Q = XL @ W[p + "self_attn.query.weight"].T + W[p + "self_attn.query.bias"]
+        K = XL @ W[p + "self_attn.key.weight"].T
+        V = XL @ W[p + "self_attn.value.weight"].T + W[p + "self_attn.value.bias"]
+        A = orc.sdpa(heads(Q), heads(K), heads(V), causal=True, fast=False).astype(np.float64)
+        A = A.transpose(1, 0, 2).reshape(n, d)
+        X = X + A @ W[p + "self_attn.out.weight"].T + W[p + "self_attn.out.bias"]
+        X = np.stack([x + npd._cross_attn(i, _ln(x, W[p + "cross_attn_ln.weight"], W[p + "cross_attn_ln.bias"]), enc)
+                      for x in X])
+        X = np.stack([x + npd._mlp(i, x) for x in X])
+    X = np.stack([_ln(x, W["decoder.ln.weight"], W["decoder.ln.bias"]) for x in X])
+    return X @ W["decoder.token_embedding.weight"].T
+
+
+def test_causal_restatement_matches_block_forward(wh, orc):
+    """The incremental textbook-mode restatement (one token per forward, k, v
+    appended to a cache) equals the same decoder run over the whole block at
+    once with the oracle's causal SDPA, row by row. Attending rows 0..pos-1 only,
+    or not appending the current k, v, fails this."""
+    tensors, meta = wh.synth.make_decoder("causal", 8, dims=(300, 128, 4, 2, 16))
+    enc = wh.synth.encoder_output("causal", 128, enc_len=40)
+    npd = NumpyDecoder(orc, tensors, meta, causal=True)
+    toks = [7, 250, 3, 3, 91, 12]
+    block = _block_logits(npd, orc, toks, enc)
+    for j in range(len(toks)):
+        got = npd.forward(toks[:j + 1], enc)
+        assert np.max(np.abs(got - block[j])) / np.max(np.abs(block[j])) < 2e-5, j
+    # the reference mask differs from the textbook one from position 1 on
+    ref = NumpyDecoder(orc, tensors, meta)
+    ref.forward(toks[:1], enc)
+    r1 = ref.forward(toks[:2], enc)
+    assert np.max(np.abs(r1 - block[1])) / np.max(np.abs(block[1])) > 1e-2
 
 
 def test_fast_exp_is_used_by_default(wh, orc):
