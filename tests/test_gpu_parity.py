@@ -105,6 +105,8 @@ MODEL_CASES = [
     ("m64q50", 6, (1000, 128, 2, 1, 40), 130),   # Q5_0, ragged last chunk
     ("hd32", 8, (777, 96, 3, 2, 32), 30),        # head size 32: generic attention
     ("f32", 0, (500, 64, 2, 1, 32), 20),         # float weights
+    ("ragT64", 8, (900, 192, 3, 1, 40), 100),    # 3 heads over 100 frames: head slabs start inside rows
+    ("ragT32", 8, (777, 96, 3, 1, 32), 31),      # the same with head size 32
 ]
 
 
@@ -209,17 +211,24 @@ def test_reference_test_fixture(wh, orc, gpu):
     assert dec.decode_tokens(enc, p) == ref.decode(enc, p)
 
 
-def test_textbook_attention_mode_vs_numpy(wh, orc, gpu):
+@pytest.mark.parametrize("dims,steps", [
+    ((800, 128, 2, 1, 96), 70),   # head size 64: LDS-tiled kernel, past one 64-key tile
+    ((600, 96, 3, 2, 80), 66),    # head size 32, two layers
+    ((500, 320, 2, 1, 40), 20),   # head size 160: the one-wave kernel
+])
+def test_textbook_attention_mode_vs_numpy(wh, orc, gpu, dims, steps):
     """Opt-in mode 1 (textbook causal mask over the KV cache) against the float64
     numpy restatement of the same forward with the oracle's fast-exp softmax,
-    for five greedy steps from position 0. The restatement is pinned on the CPU
+    at every greedy step from position 0. The restatement is pinned on the CPU
     against a whole-block forward through the oracle's causal SDPA. At position 0
     both modes see one key, so the first step equals the reference mode exactly;
     from position 1 the reference mode is far from the textbook logits."""
     from test_oracle_decoder import NumpyDecoder
 
-    tensors, meta = _model(wh, "mode1", 8, (800, 128, 2, 1, 32))
-    enc = wh.synth.encoder_output("mode1", 128, enc_len=40)
+    name = "mode1_%d_%d" % dims[1:3]
+    tensors, meta = _model(wh, name, 8, dims)
+    d = dims[1]
+    enc = wh.synth.encoder_output(name, d, enc_len=40)
     dec = wh.HIPDecoder(tensors, meta)
     dec.set_attention_mode(1)
     seq = dec.sequence([enc])
@@ -227,7 +236,7 @@ def test_textbook_attention_mode_vs_numpy(wh, orc, gpu):
     npd = NumpyDecoder(orc, tensors, meta, causal=True, fast=True)
     ref = NumpyDecoder(orc, tensors, meta, fast=True)
     toks = [1]
-    for step in range(5):
+    for step in range(steps):
         ids, lg = seq.step_greedy(logits=True)
         want = npd.forward(toks, enc)
         ref_mode = ref.forward(toks, enc)

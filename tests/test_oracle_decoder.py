@@ -23,8 +23,10 @@ def _gelu(x):
 class NumpyDecoder:
     """decoder.go restated in float64 with exact softmax. Self-attention
     follows P1/P2: only KV-cache row 0 is attended (it holds k,v only when
-    the forward ran at position 0). Cross-attention follows P3: head h, key t
-    reads row h*(T/H) + t//H, columns (t%H)*hd ... +hd of the [T, d] projection.
+    the forward ran at position 0). Cross-attention follows P3 (the [T, d]
+    projection reshaped to [H, T, hd] without a transpose): head h, key t reads
+    row (h*T + t)//H, columns ((h*T + t)%H)*hd ... +hd, also when H does not
+    divide T.
 
     causal=True is the library's opt-in textbook mode instead: every forward
     appends its k, v to the cache and head h attends to all cached rows
@@ -75,8 +77,9 @@ class NumpyDecoder:
         V = enc @ W[p + "cross_attn.value.weight"].T + W[p + "cross_attn.value.bias"]
         out = np.zeros(d)
         for h in range(H):
-            rows = h * (T // H) + np.arange(T) // H
-            cols = (np.arange(T) % H)[:, None] * hd + np.arange(hd)[None, :]
+            f = h * T + np.arange(T)  # key t of head h is hd-run f of the flat projection
+            rows = f // H
+            cols = (f % H)[:, None] * hd + np.arange(hd)[None, :]
             Kh, Vh = K[rows[:, None], cols], V[rows[:, None], cols]
             pr = self._softmax(Kh @ q[h * hd:(h + 1) * hd] / math.sqrt(hd))
             out[h * hd:(h + 1) * hd] = pr @ Vh
@@ -109,10 +112,13 @@ class NumpyDecoder:
 
 @pytest.mark.parametrize("qtype", [8, 3, 0])
 @pytest.mark.parametrize("prompt", [[11], [4, 5, 6]])
-def test_forward_matches_numpy_restatement(wh, orc, qtype, prompt):
+@pytest.mark.parametrize("enc_len", [40, 42])
+def test_forward_matches_numpy_restatement(wh, orc, qtype, prompt, enc_len):
+    """enc_len 42 is not a multiple of the 4 heads: each head's slab of the
+    flat cross K/V then starts inside a row."""
     dims = (300, 128, 4, 2, 16)
     tensors, meta = wh.synth.make_decoder(f"np{qtype}", qtype, dims=dims)
-    enc = wh.synth.encoder_output(f"np{qtype}", 128, enc_len=40)
+    enc = wh.synth.encoder_output(f"np{qtype}", 128, enc_len=enc_len)
     ref = orc.OracleModel(tensors, meta)
     ref.set_fast_exp(False)
     npd = NumpyDecoder(orc, tensors, meta)

@@ -1009,7 +1009,8 @@ int launch_layernorm(const float *x, const float *w, const float *b, float *y, i
 // KV layout per stream and layer: [2][H][ctx][hd] (K plane, then V plane).
 // mode 0 reproduces the reference mask: with Tq = 1 every key j > 0 is masked
 // (attention.go:250-256), so only cache row 0 is attended. mode 1 attends to
-// rows 0..pos (textbook causal decoding). One wavefront per (stream, head).
+// rows 0..pos (textbook causal decoding). One wavefront per (stream, head); mode 1
+// runs k_self_attn_tiled below instead where the head size allows.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(64) void k_self_attn(const float *q, const float *k, const float *v, float *kv_layer,
                                                   size_t kv_stream_stride, const int32_t *posv,
@@ -1061,10 +1062,107 @@ __global__ __launch_bounds__(64) void k_self_attn(const float *q, const float *k
     }
 }
 
+// mode 1 when hd % 4 == 0 and hd <= 128: one 256-thread block per (stream,
+// head). Keys pass through LDS in tiles of 64 rows with a row stride of hd + 1,
+// so the four lanes of a key (quarters of hd) and the 16 keys of a wave read
+// different banks; a key's quarter sums meet in two butterfly steps. Weights . V:
+// a thread owns one column and every (256 / hd)-th key, and the column partials
+// are summed through LDS. Row pos of the cache is written here and read from the
+// fresh k, v instead.
+constexpr int SA_TILE = 64;
+
+__host__ __device__ constexpr size_t self_attn_tiled_lds(int hd, int ctx) {
+    return sizeof(float) * ((size_t)hd + (size_t)SA_TILE * (hd + 1) + (size_t)ctx + 8 + 256);
+}
+
+__global__ __launch_bounds__(256) void k_self_attn_tiled(const float *q, const float *k, const float *v,
+                                                         float *kv_layer, size_t kv_stream_stride,
+                                                         const int32_t *posv, const int32_t *active, float *out,
+                                                         int H, int hd, int ctx, float scale) {
+    extern __shared__ float sm[];
+    const int s = blockIdx.x / H, h = blockIdx.x % H, t = threadIdx.x;
+    if (active && !active[s]) return;
+    const int d = H * hd, p = posv[s], n = p + 1;
+    float *Kc = kv_layer + (size_t)s * kv_stream_stride + (size_t)h * ctx * hd;
+    float *Vc = Kc + (size_t)H * ctx * hd;
+    const float *qh = q + (size_t)s * d + (size_t)h * hd;
+    const float *kh = k + (size_t)s * d + (size_t)h * hd;
+    const float *vh = v + (size_t)s * d + (size_t)h * hd;
+    float *qs = sm, *tile = qs + hd, *sc = tile + SA_TILE * (hd + 1), *red = sc + ctx, *part = red + 8;
+    for (int j = t; j < hd; j += 256) {
+        Kc[(size_t)p * hd + j] = kh[j];
+        Vc[(size_t)p * hd + j] = vh[j];
+        qs[j] = qh[j];
+    }
+    const int r = t >> 2, qt = t & 3, qlen = hd >> 2;
+    float mx = -INFINITY;
+    for (int t0 = 0; t0 < n; t0 += SA_TILE) {
+        const int nk = min(SA_TILE, n - t0);
+        __syncthreads();  // the previous tile is consumed (and qs is written)
+        for (int e = t; e < nk * qlen; e += 256) {
+            const int rr = e / qlen, c4 = e - rr * qlen, key = t0 + rr;
+            const float4 x = *reinterpret_cast<const float4 *>((key == p ? kh : Kc + (size_t)key * hd) + 4 * c4);
+            float *dst = tile + rr * (hd + 1) + 4 * c4;
+            dst[0] = x.x;
+            dst[1] = x.y;
+            dst[2] = x.z;
+            dst[3] = x.w;
+        }
+        __syncthreads();
+        float acc = 0.0f;
+        if (r < nk) {
+            const float *row = tile + r * (hd + 1) + qt * qlen;
+            const float *qq = qs + qt * qlen;
+            for (int c = 0; c < qlen; c++) acc += qq[c] * row[c];
+        }
+        acc = group_sum<4>(acc);
+        if (r < nk && qt == 0) {
+            const float sco = acc * scale;
+            sc[t0 + r] = sco;
+            mx = fmaxf(mx, sco);
+        }
+    }
+    mx = group_max<64>(mx);
+    __syncthreads();
+    if ((t & 63) == 0) red[t >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float sum = 0.0f;
+    for (int i = t; i < n; i += 256) {
+        const float e = fast_exp(sc[i] - mx);
+        sc[i] = e;
+        sum += e;
+    }
+    sum = block_sum256(sum, red + 4);
+    const bool uniform = (sum == 0.0f);
+    const float inv = uniform ? 1.0f / (float)n : 1.0f / sum;
+    const int G = 256 / hd, g = t / hd, c = t - g * hd;
+    if (g < G) {
+        float o = 0.0f;
+        for (int i = g; i < n; i += G) {
+            const float *vr = (i == p) ? vh : Vc + (size_t)i * hd;
+            o += (uniform ? inv : sc[i] * inv) * vr[c];
+        }
+        part[g * hd + c] = o;
+    }
+    __syncthreads();
+    if (t < hd) {
+        float o = 0.0f;
+        for (int i = 0; i < G; i++) o += part[i * hd + t];
+        out[(size_t)s * d + (size_t)h * hd + t] = o;
+    }
+}
+
 int launch_self_attn(const float *q, const float *k, const float *v, float *kv_layer, size_t kv_stream_stride,
                      const int32_t *pos, const int32_t *active, float *out, int S, int H, int hd, int ctx, int mode,
                      hipStream_t st) {
     float scale = (float)(1.0 / sqrt((double)hd));
+    if (mode == 1 && hd % 4 == 0 && hd <= 128 && self_attn_tiled_lds(hd, ctx) <= 65536) {
+        hipLaunchKernelGGL(k_self_attn_tiled, dim3(S * H), dim3(256), self_attn_tiled_lds(hd, ctx), st, q, k, v,
+                           kv_layer, kv_stream_stride, pos, active, out, H, hd, ctx, scale);
+        WH_HIP(hipGetLastError());
+        return WH_OK;
+    }
     size_t shmem = sizeof(float) * (size_t)(mode == 0 ? 1 : ctx);
     hipLaunchKernelGGL(k_self_attn, dim3(S * H), dim3(64), shmem, st, q, k, v, kv_layer, kv_stream_stride, pos,
                        active, out, H, hd, ctx, mode, scale);
