@@ -195,6 +195,32 @@ def test_batch_equals_single_streams(wh, orc, gpu):
         assert got[i] == ref.decode(encs[i], params[i]), i
 
 
+@pytest.mark.parametrize("qtype", [3, 8])
+def test_sixteen_streams_split_gemv_vs_oracle(wh, orc, gpu, qtype):
+    """16 streams on the multi-kernel chain: the matrix-core GEMV at batch 16 with
+    K split over several workgroups per 16-row tile (2 ranges of the 512-column
+    rows, 4 of the 2048-column fc2 rows), the last workgroup of a tile summing the
+    partial tiles; every stream's logits at every step against the oracle."""
+    name = f"s16split{qtype}"
+    tensors, meta = _model(wh, name, qtype, (1000, 512, 8, 2, 64))
+    encs = [wh.synth.encoder_output(name, 512, stream=i, enc_len=48) for i in range(16)]
+    dec = wh.HIPDecoder(tensors, meta)
+    ref = orc.OracleModel(tensors, meta)
+    seq = dec.sequence(encs)
+    prompts = [[3 + i, 7, 11 + 2 * i][:1 + i % 3] for i in range(16)]
+    for i, p in enumerate(prompts):
+        seq.set_tokens(i, p)
+    states = [ref.state(p) for p in prompts]
+    for step in range(4):
+        ids, lg = seq.step_greedy(logits=True)
+        for i in range(16):
+            want = states[i].forward(encs[i])
+            assert rel_err(lg[i], want) < LOGIT_TOL, (step, i, rel_err(lg[i], want))
+            states[i].push(ids[i])
+    seq.close()
+    dec.close()
+
+
 def test_reference_test_fixture(wh, orc, gpu):
     """internal/model/decoder_test.go:89-180 on the device: d=4, 2 heads of 2,
     8 encoder frames, V=51865; greedy and beam return non-empty segments and

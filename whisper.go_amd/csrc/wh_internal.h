@@ -114,9 +114,21 @@ struct GemvIn {
     const float *x = nullptr;  // [batch, ldx]
     int32_t ldx = 0;
 };
-// Up to 3 matrices of the same type in one launch (e.g. q,k,v).
+// Workspace of the batched matrix-core GEMV's split-K path, owned by one stream of
+// launches: partial tiles of at most `tiles` 16-row tiles as {launch number, value}
+// pairs (zero when allocated) and one arrival counter per tile (zero when
+// allocated; the kernel leaves it zero). `seq` numbers the launches.
+constexpr int GEMVM_MAX_SPLIT = 4;
+struct GemvWork {
+    uint64_t *part = nullptr;  // tiles * GEMVM_MAX_SPLIT * 256 pairs
+    uint32_t *cnt = nullptr;   // tiles counters
+    int tiles = 0;
+    uint32_t seq = 0;
+};
+// Up to 3 matrices of the same type in one launch (e.g. q,k,v). `work` (optional)
+// lets batches of 6..16 rows split K over more workgroups.
 int launch_gemv(const DevMat *const *mats, const GemvIn *in, const GemvOut *out, int nmat, int batch,
-                hipStream_t st);
+                hipStream_t st, GemvWork *work = nullptr);
 int launch_dequant_rows(const DevMat &m, int32_t row0, int32_t nrows, float *out, hipStream_t st);
 // wh_dequantize with every staging buffer in a file-scope device array (wh_noalloc.hip).
 int dequantize_noalloc(uint32_t type, const void *raw, uint64_t nbytes, uint64_t n, float *out, int32_t device);

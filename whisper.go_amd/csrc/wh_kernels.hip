@@ -40,10 +40,15 @@ struct GemvOpDev {
     int32_t ldres;
     int32_t gelu;
     int32_t row_begin;
+    int32_t tile_begin;  // first 16-row tile of this op in the split-K workspace
 };
 struct GemvArgs {
     GemvOpDev op[3];
     int32_t nop, batch, total_rows;
+    int32_t nsplit;       // k_gemv_mfma: K ranges per row tile (1 = no split)
+    uint32_t seq;         // launch number of the workspace (the tag of this launch's partials)
+    uint64_t *part;       // [tile][nsplit][256] {tag, value} partial tiles when nsplit > 1
+    uint32_t *cnt;        // [tile] arrivals, zero between launches
 };
 
 // Decode block `blk` of a row into integer-valued floats q[32] and return the
@@ -533,6 +538,12 @@ __global__ __launch_bounds__(256) void k_gemv2(GemvArgs a, int ch) {
 #ifndef GEMVM_NW_SMALL
 #define GEMVM_NW_SMALL 16  // waves per workgroup for matrices of at most 2048 rows
 #endif
+#ifndef GEMVM_CH_SMALL
+#define GEMVM_CH_SMALL 56  // blocks staged per round for matrices of at most 2048 rows
+#endif
+#ifndef GEMVM_WG_TARGET
+#define GEMVM_WG_TARGET 256  // split K up to this many workgroups
+#endif
 
 typedef float gemvm_f4 __attribute__((ext_vector_type(4)));
 
@@ -569,9 +580,12 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_mfma(GemvArgs a) {
     const int row = min(r0 + lr, op.rows - 1);  // past the last row: re-read it, drop it
     float *sxs = xm + CH * 512;
     const bool vec = (((uintptr_t)op.x) & 15) == 0 && (op.ldx & 3) == 0 && (op.cols & 3) == 0;
+    // this workgroup's blocks: split z of a.nsplit equal runs of the row
+    const int nsplit = a.nsplit, split = blockIdx.z, per = (nb + nsplit - 1) / nsplit;
+    const int kb0 = min(nb, split * per), kb1 = min(nb, kb0 + per);
     gemvm_f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int cb = 0; cb < nb; cb += CH) {
-        const int nbc = min(CH, nb - cb);
+    for (int cb = kb0; cb < kb1; cb += CH) {
+        const int nbc = min(CH, kb1 - cb);
         // this wave's blocks of the chunk (cb + wave + NW u): raw loads first
         RawBlk rb[NBW];
 #pragma unroll
@@ -661,10 +675,54 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_mfma(GemvArgs a) {
         for (int i = 0; i < 4; i++) outs[(4 * kq + i) * 16 + lr] = sum[i];
     }
     __syncthreads();
+    float v = tid < 256 ? outs[tid] : 0.0f;
+    if (nsplit > 1) {
+        // Split K: every split stores its tile as {launch number, value} pairs and
+        // counts itself in; the workgroup that arrives last sums the nsplit tiles
+        // in split order (the same sum whatever the arrival order) and runs the
+        // epilogue. No fences (on this chip they write back or drop the whole L2):
+        // the pairs are stored and read at agent scope, and the last workgroup
+        // reads each pair until it carries this launch's number (a pair from a
+        // workgroup already counted is in flight, so the bounded wait ends at
+        // once; a pair that never arrives gives NaN). The counter goes back to 0.
+        __shared__ int last;
+        const int tile = op.tile_begin + blockIdx.x;
+        uint64_t *pt = a.part + (size_t)tile * nsplit * 256;
+        const uint64_t tag = (uint64_t)a.seq << 32;
+        if (tid < 256)
+            __hip_atomic_store(pt + split * 256 + tid, tag | __float_as_uint(v), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (tid == 0)
+            last = __hip_atomic_fetch_add(a.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   (uint32_t)(nsplit - 1);
+        __syncthreads();
+        if (!last) return;
+        if (tid < 256) {
+            float sum = 0.0f;
+            for (int j = 0; j < nsplit; j++) {
+                float pj = v;
+                if (j != split) {
+                    uint64_t pr = __hip_atomic_load(pt + j * 256 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    for (int spin = 0; (pr & 0xffffffff00000000ull) != tag; spin++) {
+                        if (spin >= (1 << 20)) {
+                            pr = tag | 0x7fc00000u;  // NaN
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(1);
+                        pr = __hip_atomic_load(pt + j * 256 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                    pj = __uint_as_float((uint32_t)pr);
+                }
+                sum += pj;
+            }
+            v = sum;
+        }
+        if (tid == 0) __hip_atomic_store(a.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     if (tid < 256) {
         const int b = tid >> 4, r = r0 + (tid & 15);
         if (b < batch && r < op.rows) {
-            float v = outs[tid];
             if (op.bias) v = v + op.bias[r];
             if (op.gelu) v = gelu_ref(v);
             if (op.res) v = op.res[(size_t)b * op.ldres + r] + v;
@@ -674,10 +732,28 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_mfma(GemvArgs a) {
 }
 
 template <int TYPE>
-static bool gemvm_launch(const GemvArgs &a, int maxrows, hipStream_t st) {
+static bool gemvm_launch(GemvArgs &a, int maxrows, GemvWork *work, hipStream_t st) {
     if (a.batch < GEMVM_MIN_BATCH || a.batch > 16) return false;
-    const dim3 grid((maxrows + 15) / 16, a.nop);
-    constexpr size_t lds40 = (size_t)40 * (512 + 16) * 4;
+    // split K while the row tiles of the launch are too few to give every CU a
+    // workgroup (matrices of at most 2048 rows, with a workspace)
+    int tiles = 0;
+    for (int i = 0; i < a.nop; i++) tiles += (a.op[i].rows + 15) / 16;
+    a.nsplit = 1;
+    if (work && work->part && maxrows <= 2048 && tiles <= work->tiles) {
+        int nsplit = GEMVM_WG_TARGET / tiles;
+        int nbmin = a.op[0].nb;
+        for (int i = 1; i < a.nop; i++) nbmin = std::min(nbmin, a.op[i].nb);
+        nsplit = std::min(std::min(nsplit, GEMVM_MAX_SPLIT), std::max(1, nbmin / 8));
+        if (nsplit > 1) {
+            a.nsplit = nsplit;
+            a.part = work->part;
+            a.cnt = work->cnt;
+            a.seq = ++work->seq;
+            if (a.seq == 0) a.seq = ++work->seq;  // 0 is the tag of the zeroed buffer
+        }
+    }
+    const dim3 grid((maxrows + 15) / 16, a.nop, a.nsplit);
+    constexpr size_t lds40 = (size_t)GEMVM_CH_SMALL * (512 + 16) * 4;
     // the dynamic LDS above the default 64 KiB, asked once per device (bit d of
     // `granted`); refused: 20-block chunks
     static std::atomic<uint32_t> granted{0};
@@ -686,7 +762,7 @@ static bool gemvm_launch(const GemvArgs &a, int maxrows, hipStream_t st) {
         int dev = 0;
         if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 32) {
             big = (granted.load() >> dev) & 1u;
-            if (!big && hipFuncSetAttribute((const void *)k_gemv_mfma<TYPE, 40, GEMVM_NW_SMALL>,
+            if (!big && hipFuncSetAttribute((const void *)k_gemv_mfma<TYPE, GEMVM_CH_SMALL, GEMVM_NW_SMALL>,
                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds40) == hipSuccess) {
                 granted.fetch_or(1u << dev);
                 big = true;
@@ -694,7 +770,7 @@ static bool gemvm_launch(const GemvArgs &a, int maxrows, hipStream_t st) {
         }
     }
     if (big) {
-        hipLaunchKernelGGL((k_gemv_mfma<TYPE, 40, GEMVM_NW_SMALL>), grid, dim3(64 * GEMVM_NW_SMALL), lds40, st, a);
+        hipLaunchKernelGGL((k_gemv_mfma<TYPE, GEMVM_CH_SMALL, GEMVM_NW_SMALL>), grid, dim3(64 * GEMVM_NW_SMALL), lds40, st, a);
     } else {
         hipLaunchKernelGGL((k_gemv_mfma<TYPE, 20, 4>), grid, dim3(256), (size_t)20 * (512 + 16) * 4, st, a);
     }
@@ -794,7 +870,7 @@ static void gemv_launch_type(const GemvArgs &a, int nb, bool safe, hipStream_t s
 }
 
 int launch_gemv(const DevMat *const *mats, const GemvIn *in, const GemvOut *out, int nmat, int batch,
-                hipStream_t st) {
+                hipStream_t st, GemvWork *work) {
     if (nmat < 1 || nmat > 3) return fail(WH_ERR_INVALID, "gemv: 1..3 matrices per launch");
     if (batch < 1 || batch > 16) return fail(WH_ERR_INVALID, "gemv: batch must be in [1,16]");
     GemvArgs a;
@@ -823,6 +899,7 @@ int launch_gemv(const DevMat *const *mats, const GemvIn *in, const GemvOut *out,
         o.ldres = out[i].ldres;
         o.gelu = out[i].gelu;
         o.row_begin = total;
+        o.tile_begin = i == 0 ? 0 : a.op[i - 1].tile_begin + (a.op[i - 1].rows + 15) / 16;
         total += m.rows;
         if (m.nb > nbmax) nbmax = m.nb;
         if (m.rows > maxrows) maxrows = m.rows;
@@ -831,11 +908,11 @@ int launch_gemv(const DevMat *const *mats, const GemvIn *in, const GemvOut *out,
     a.total_rows = total;
     bool done = false;
     switch (type) {
-    case 2: done = gemv2_launch<2>(a, maxrows, nbmax, st) || gemvm_launch<2>(a, maxrows, st); break;
-    case 3: done = gemv2_launch<3>(a, maxrows, nbmax, st) || gemvm_launch<3>(a, maxrows, st); break;
-    case 6: done = gemv2_launch<6>(a, maxrows, nbmax, st) || gemvm_launch<6>(a, maxrows, st); break;
-    case 7: done = gemv2_launch<7>(a, maxrows, nbmax, st) || gemvm_launch<7>(a, maxrows, st); break;
-    case 8: done = gemv2_launch<8>(a, maxrows, nbmax, st) || gemvm_launch<8>(a, maxrows, st); break;
+    case 2: done = gemv2_launch<2>(a, maxrows, nbmax, st) || gemvm_launch<2>(a, maxrows, work, st); break;
+    case 3: done = gemv2_launch<3>(a, maxrows, nbmax, st) || gemvm_launch<3>(a, maxrows, work, st); break;
+    case 6: done = gemv2_launch<6>(a, maxrows, nbmax, st) || gemvm_launch<6>(a, maxrows, work, st); break;
+    case 7: done = gemv2_launch<7>(a, maxrows, nbmax, st) || gemvm_launch<7>(a, maxrows, work, st); break;
+    case 8: done = gemv2_launch<8>(a, maxrows, nbmax, st) || gemvm_launch<8>(a, maxrows, work, st); break;
     default: break;
     }
     if (!done) {
@@ -1192,13 +1269,21 @@ __global__ __launch_bounds__(256) void k_cross_scores64(const float *q, const fl
     const float4 q4 = ((const float4 *)(q + (size_t)s * d + h * 64))[slot];
     const float *K = kbase[s] + (size_t)h * enc_len * 64;
     const int t0 = c * CROSS_CHUNK, t1 = min(t0 + CROSS_CHUNK, enc_len);
+    // each 16-lane group takes keys tb, tb + 16, ...: all CROSS_CHUNK / 16 key rows
+    // are loaded before the first dot product, so a wave keeps 8 KiB in flight
+    constexpr int U = CROSS_CHUNK / 16;
+    const int tb = t0 + wave * 4 + (lane >> 4);
+    float4 k4[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int t = tb + 16 * u;
+        k4[u] = t < t1 ? ((const float4 *)(K + (size_t)t * 64))[slot] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     float mx = -INFINITY;
-    for (int t = t0 + wave * 4 + (lane >> 4); t - (lane >> 4) < t1; t += 16) {
-        float part = 0.0f;
-        if (t < t1) {
-            float4 k4 = ((const float4 *)(K + (size_t)t * 64))[slot];
-            part = q4.x * k4.x + q4.y * k4.y + q4.z * k4.z + q4.w * k4.w;
-        }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int t = tb + 16 * u;
+        float part = q4.x * k4[u].x + q4.y * k4[u].y + q4.z * k4[u].z + q4.w * k4[u].w;
         float dot = group_sum<16>(part);
         if (t < t1) {
             float sco = dot * scale;
@@ -1228,11 +1313,25 @@ __global__ __launch_bounds__(256) void k_cross_pv64(const float *const *vbase, c
     const int t0 = c * CROSS_CHUNK, t1 = min(t0 + CROSS_CHUNK, enc_len);
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     float es = 0.0f;
-    for (int t = t0 + wave * 4 + (lane >> 4); t < t1; t += 16) {
-        float e = fast_exp(sc[t] - M);
-        float4 v4 = ((const float4 *)(V + (size_t)t * 64))[slot];
-        acc.x += e * v4.x; acc.y += e * v4.y; acc.z += e * v4.z; acc.w += e * v4.w;
-        if (slot == 0) es += e;
+    // all of a lane's V rows and scores are loaded first (8 KiB in flight per
+    // wave), then summed in key order
+    constexpr int U = CROSS_CHUNK / 16;
+    const int tb = t0 + wave * 4 + (lane >> 4);
+    float4 v4[U];
+    float sv[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int t = tb + 16 * u;
+        v4[u] = t < t1 ? ((const float4 *)(V + (size_t)t * 64))[slot] : make_float4(0.f, 0.f, 0.f, 0.f);
+        sv[u] = t < t1 ? sc[t] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        if (tb + 16 * u < t1) {
+            float e = fast_exp(sv[u] - M);
+            acc.x += e * v4[u].x; acc.y += e * v4[u].y; acc.z += e * v4[u].z; acc.w += e * v4[u].w;
+            if (slot == 0) es += e;
+        }
     }
     // reduce the 4 key groups of the wave (lanes differing in bits 4,5)
 #pragma unroll

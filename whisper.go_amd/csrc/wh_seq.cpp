@@ -36,6 +36,7 @@ struct wh_seq {
     std::vector<void *> allocs;
     float *x = nullptr, *xln = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *h = nullptr;
     float *logits = nullptr;
+    wh::GemvWork gw{};  // split-K workspace of the batched GEMV (6..16 streams)
     float *kv = nullptr;
     size_t kv_stream = 0, kv_layer = 0;  // floats
     float *crossK = nullptr, *crossV = nullptr;
@@ -205,7 +206,7 @@ int seq_forward(wh_seq &s) {
         GemvOut out;
         out.y = y; out.ldy = ldy; out.bias = bias; out.res = res; out.ldres = ldy; out.gelu = gelu;
         Prof p(s, "gemv", mat_bytes(w));
-        return launch_gemv(&mat, &in, &out, 1, S, st);
+        return launch_gemv(&mat, &in, &out, 1, S, st, &s.gw);
     };
     {
         Prof p(s, "embed", 0);
@@ -226,7 +227,7 @@ int seq_forward(wh_seq &s) {
             out[1].y = s.k; out[1].ldy = d;
             out[2].y = s.v; out[2].ldy = d; out[2].bias = l.svb;
             Prof p(s, "gemv", mat_bytes(l.sq) + mat_bytes(l.sk) + mat_bytes(l.sv));
-            if ((rc = launch_gemv(mats, in, out, 3, S, st))) return rc;
+            if ((rc = launch_gemv(mats, in, out, 3, S, st, &s.gw))) return rc;
         } else {
             if ((rc = gemv1(l.sq, s.xln, d, s.q, d, l.sqb, nullptr, 0))) return rc;
             if ((rc = gemv1(l.sk, s.xln, d, s.k, d, nullptr, nullptr, 0))) return rc;
@@ -696,6 +697,14 @@ int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t e
     ALLOC(s->topk_lp, (size_t)S * 8);
     ALLOC(s->topk_logz, (size_t)S);
     ALLOC(s->topk_part, (size_t)TOPK_SCRATCH_FLOATS);
+    if (S >= 6) {
+        // split-K workspace of the batched GEMV: up to 128 row tiles are split
+        s->gw.tiles = 128;
+        ALLOC(s->gw.part, (size_t)s->gw.tiles * GEMVM_MAX_SPLIT * 256);
+        ALLOC(s->gw.cnt, (size_t)s->gw.tiles);
+        WH_HIP(hipMemsetAsync(s->gw.part, 0, sizeof(uint64_t) * s->gw.tiles * GEMVM_MAX_SPLIT * 256, s->st));
+        WH_HIP(hipMemsetAsync(s->gw.cnt, 0, sizeof(uint32_t) * s->gw.tiles, s->st));
+    }
 #undef ALLOC
     WH_HIP(hipMemsetAsync(s->hist_len, 0, sizeof(int32_t) * S, s->st));
     WH_HIP(hipMemsetAsync(s->tok, 0, sizeof(int32_t) * S, s->st));
