@@ -541,6 +541,15 @@ __global__ __launch_bounds__(256) void k_gemv2(GemvArgs a, int ch) {
 #ifndef GEMVM_CH_SMALL
 #define GEMVM_CH_SMALL 56  // blocks staged per round for matrices of at most 2048 rows
 #endif
+#ifndef GEMVM_SMALL_ROWS
+#define GEMVM_SMALL_ROWS 2048  // matrices up to this many rows use the CH_SMALL, NW_SMALL kernel
+#endif
+#ifndef GEMVM_CH_TALL
+#define GEMVM_CH_TALL 20
+#endif
+#ifndef GEMVM_NW_TALL
+#define GEMVM_NW_TALL 10
+#endif
 #ifndef GEMVM_WG_TARGET
 #define GEMVM_WG_TARGET 256  // split K up to this many workgroups
 #endif
@@ -731,6 +740,20 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_mfma(GemvArgs a) {
     }
 }
 
+// Dynamic LDS above the default 64 KiB for one kernel, asked once per device and
+// remembered per (weight type, kernel slot K, device) in a bit set; true when granted.
+template <int TYPE, int K>
+static bool gemvm_lds_granted(const void *kern, size_t lds) {
+    if (lds <= 65536) return true;
+    static std::atomic<uint32_t> granted{0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 32) return false;
+    if ((granted.load() >> dev) & 1u) return true;
+    if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) return false;
+    granted.fetch_or(1u << dev);
+    return true;
+}
+
 template <int TYPE>
 static bool gemvm_launch(GemvArgs &a, int maxrows, GemvWork *work, hipStream_t st) {
     if (a.batch < GEMVM_MIN_BATCH || a.batch > 16) return false;
@@ -739,7 +762,7 @@ static bool gemvm_launch(GemvArgs &a, int maxrows, GemvWork *work, hipStream_t s
     int tiles = 0;
     for (int i = 0; i < a.nop; i++) tiles += (a.op[i].rows + 15) / 16;
     a.nsplit = 1;
-    if (work && work->part && maxrows <= 2048 && tiles <= work->tiles) {
+    if (work && work->part && maxrows <= GEMVM_SMALL_ROWS && tiles <= work->tiles) {
         int nsplit = GEMVM_WG_TARGET / tiles;
         int nbmin = a.op[0].nb;
         for (int i = 1; i < a.nop; i++) nbmin = std::min(nbmin, a.op[i].nb);
@@ -753,27 +776,23 @@ static bool gemvm_launch(GemvArgs &a, int maxrows, GemvWork *work, hipStream_t s
         }
     }
     const dim3 grid((maxrows + 15) / 16, a.nop, a.nsplit);
-    constexpr size_t lds40 = (size_t)GEMVM_CH_SMALL * (512 + 16) * 4;
-    // the dynamic LDS above the default 64 KiB, asked once per device (bit d of
-    // `granted`); refused: 20-block chunks
-    static std::atomic<uint32_t> granted{0};
-    bool big = false;
-    if (maxrows <= 2048) {
-        int dev = 0;
-        if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 32) {
-            big = (granted.load() >> dev) & 1u;
-            if (!big && hipFuncSetAttribute((const void *)k_gemv_mfma<TYPE, GEMVM_CH_SMALL, GEMVM_NW_SMALL>,
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds40) == hipSuccess) {
-                granted.fetch_or(1u << dev);
-                big = true;
-            }
+    if (maxrows <= GEMVM_SMALL_ROWS) {
+        constexpr size_t lds = (size_t)GEMVM_CH_SMALL * (512 + 16) * 4;
+        if (gemvm_lds_granted<TYPE, 0>((const void *)k_gemv_mfma<TYPE, GEMVM_CH_SMALL, GEMVM_NW_SMALL>, lds)) {
+            hipLaunchKernelGGL((k_gemv_mfma<TYPE, GEMVM_CH_SMALL, GEMVM_NW_SMALL>), grid, dim3(64 * GEMVM_NW_SMALL),
+                               lds, st, a);
+            return true;
+        }
+    } else {
+        constexpr size_t lds = (size_t)GEMVM_CH_TALL * (512 + 16) * 4;
+        if (gemvm_lds_granted<TYPE, 1>((const void *)k_gemv_mfma<TYPE, GEMVM_CH_TALL, GEMVM_NW_TALL>, lds)) {
+            hipLaunchKernelGGL((k_gemv_mfma<TYPE, GEMVM_CH_TALL, GEMVM_NW_TALL>), grid, dim3(64 * GEMVM_NW_TALL), lds,
+                               st, a);
+            return true;
         }
     }
-    if (big) {
-        hipLaunchKernelGGL((k_gemv_mfma<TYPE, GEMVM_CH_SMALL, GEMVM_NW_SMALL>), grid, dim3(64 * GEMVM_NW_SMALL), lds40, st, a);
-    } else {
-        hipLaunchKernelGGL((k_gemv_mfma<TYPE, 20, 4>), grid, dim3(256), (size_t)20 * (512 + 16) * 4, st, a);
-    }
+    // LDS above 64 KiB refused: 20-block chunks
+    hipLaunchKernelGGL((k_gemv_mfma<TYPE, 20, 4>), grid, dim3(256), (size_t)20 * (512 + 16) * 4, st, a);
     return true;
 }
 
