@@ -195,7 +195,7 @@ def test_batch_equals_single_streams(wh, orc, gpu):
         assert got[i] == ref.decode(encs[i], params[i]), i
 
 
-@pytest.mark.parametrize("qtype", [3, 8])
+@pytest.mark.parametrize("qtype", [3, 8, 2, 6, 7])
 def test_sixteen_streams_split_gemv_vs_oracle(wh, orc, gpu, qtype):
     """16 streams on the multi-kernel chain: the matrix-core GEMV at batch 16 with
     K split over several workgroups per 16-row tile (2 ranges of the 512-column
