@@ -179,11 +179,12 @@ int launch_argmax_final(const SampleBufs &b, const float *cur, int S, int V, int
 int launch_topk_ties(const float *cur, const int32_t *active, int S, int V, int k, int kk, float inv_temp,
                      const float *logz, int32_t *tok, float *lp, hipStream_t st);
 // One beam step's candidate ranking (Go's sort.Slice order), prune and in-place
-// reuse of the beam objects' histories on the device.
+// reuse of the beam objects' histories on the device. `step` is recorded in
+// stop[3] when the step stops the search or finds a position past the context.
 int launch_beam_select(const int32_t *ttok, const float *tlp, int k, int kk, int32_t *hist, int32_t *len,
                        int32_t *gcap, int cap, float *score, int32_t *order, int32_t *nbeams, int32_t *active,
                        int32_t *tok, int32_t *pos, int32_t *stop, const float *powtab, int bs, int eot, int n_ctx,
-                       hipStream_t st);
+                       int step, hipStream_t st);
 // top-k scratch: TOPK_ROWS_MAX x TOPK_PARTS partitions x (2 + 2 * 8) floats
 constexpr int TOPK_ROWS_MAX = 16, TOPK_PARTS = 32, TOPK_SCRATCH_FLOATS = TOPK_ROWS_MAX * TOPK_PARTS * 18;
 int launch_topk(const float *cur, const int32_t *active, int S, int V, int k, float inv_temp, int32_t *out_tok,

@@ -2199,13 +2199,15 @@ struct GoSort {
 // last token more than 20 times (decoder.go:690-718). stop[1] is the position
 // of the first live hypothesis at or past n_ctx (the reference's forward fails
 // there on the next step), else -1; such a hypothesis is not made active.
-// powtab[n] = float(pow(n, 0.6)) as the host computes it. A stopped state is left
-// as it is.
+// powtab[n] = float(pow(n, 0.6)) as the host computes it. stop[3] is the step
+// (the host's loop index `step`) that set stop[0] or stop[1]. A stopped state,
+// or one with stop[1] set, is left as it is, so the host may queue several steps
+// before it reads the flags.
 __global__ __launch_bounds__(256) void k_beam_select(const int32_t *ttok, const float *tlp, int k, int kk,
                                                      int32_t *hist, int32_t *len, int32_t *gcap, int cap,
                                                      float *score, int32_t *order, int32_t *nbeams, int32_t *active,
                                                      int32_t *tok, int32_t *pos, int32_t *stop, const float *powtab,
-                                                     int bs, int eot, int n_ctx) {
+                                                     int bs, int eot, int n_ctx, int step) {
     constexpr int NCAND = BEAM_MAX * (TOPK_MAX - 1);
     __shared__ float cnorm[NCAND], cscore[NCAND], clp[NCAND];
     __shared__ int cpar[NCAND], ctok[NCAND], cix[NCAND];
@@ -2219,7 +2221,7 @@ __global__ __launch_bounds__(256) void k_beam_select(const int32_t *ttok, const 
     __shared__ int ttoks[BEAM_MAX * TOPK_MAX];
     __shared__ int nkeep, nbin, s_nb, s_par, s_cpy, s_zero, s_bad;
     const int t = threadIdx.x;
-    if (stop[0]) return;
+    if (stop[0] || stop[1] >= 0) return;
     if (t < bs) {
         blen[t] = len[t];
         bcap[t] = gcap[t];
@@ -2327,6 +2329,7 @@ __global__ __launch_bounds__(256) void k_beam_select(const int32_t *ttok, const 
         stop[0] = halt ? 1 : (s_bad ? 1 : 0);
         stop[1] = bad_pos;
         stop[2] = s_bad;
+        if (halt || s_bad || bad_pos >= 0) stop[3] = step;
     }
 }
 
@@ -2341,11 +2344,11 @@ int launch_topk_ties(const float *cur, const int32_t *active, int S, int V, int 
 int launch_beam_select(const int32_t *ttok, const float *tlp, int k, int kk, int32_t *hist, int32_t *len,
                        int32_t *gcap, int cap, float *score, int32_t *order, int32_t *nbeams, int32_t *active,
                        int32_t *tok, int32_t *pos, int32_t *stop, const float *powtab, int bs, int eot, int n_ctx,
-                       hipStream_t st) {
+                       int step, hipStream_t st) {
     if (bs < 1 || bs > BEAM_MAX || k < 1 || k >= kk || kk > TOPK_MAX)
         return fail(WH_ERR_INVALID, "beam: unsupported beam size");
     hipLaunchKernelGGL(k_beam_select, dim3(1), dim3(256), 0, st, ttok, tlp, k, kk, hist, len, gcap, cap, score, order,
-                       nbeams, active, tok, pos, stop, powtab, bs, eot, n_ctx);
+                       nbeams, active, tok, pos, stop, powtab, bs, eot, n_ctx, step);
     WH_HIP(hipGetLastError());
     return WH_OK;
 }

@@ -1139,6 +1139,9 @@ int decode_greedy_batch(const wh_model *m, int32_t S, const float *const *encs, 
 // (launch_topk, plus the reference's scan for rows with ties), candidate ranking
 // in Go's sort.Slice order, and the prune with the reference's in-place reuse of
 // the beam objects (k_beam_select). The host reads the stop words once per step.
+// Beam steps queued between two reads of the stop flags.
+constexpr int BEAM_SYNC = 4;
+
 int decode_beam(const wh_model *m, const float *enc, int32_t enc_len, int32_t enc_dim, const wh_decode_params *p,
                 int32_t *out_tokens, int32_t cap, int32_t *out_len, const volatile int32_t *cancel, int32_t dev) {
     if (!p) return fail(WH_ERR_INVALID, "model: decode: null params");
@@ -1225,19 +1228,26 @@ int decode_beam(const wh_model *m, const float *enc, int32_t enc_len, int32_t en
             (rc = launch_topk(q.sb.cur, q.active, bs, V, KK, inv, q.topk_tok, q.topk_lp, q.topk_logz, q.topk_part, q.st)) ||
             (rc = launch_topk_ties(q.sb.cur, q.active, bs, V, K, KK, inv, q.topk_logz, q.topk_tok, q.topk_lp, q.st)) ||
             (rc = launch_beam_select(q.topk_tok, q.topk_lp, K, KK, q.hist, q.hist_len, gcap, hc, score, order, nbeams,
-                                     q.active, q.tok, q.pos, stop, powtab, bs, eot, m->n_ctx, q.st)))
+                                     q.active, q.tok, q.pos, stop, powtab, bs, eot, m->n_ctx, step, q.st)))
             return fail(rc, std::string("model: decode: beam search forward: ") + wh_last_error());
-        WH_HIP(hipMemcpyAsync(q.pinned_ids, stop, sizeof(int32_t) * 3, hipMemcpyDeviceToHost, q.st));
+        // The flags are read every BEAM_SYNC steps and after the last: a step after
+        // the one that set them leaves the beams as they are (k_beam_select), and
+        // stop[3] names that step, so the outcome is the one of a check per step.
+        if ((step + 1) % BEAM_SYNC != 0 && step + 1 < mt) continue;
+        WH_HIP(hipMemcpyAsync(q.pinned_ids, stop, sizeof(int32_t) * 4, hipMemcpyDeviceToHost, q.st));
         WH_HIP(hipStreamSynchronize(q.st));
-        g_decode_steps++;
         if ((rc = batch_check(q))) return fail(rc, std::string("model: decode: beam search forward: ") + wh_last_error());
         if (q.prof) q.prof_resolve();
+        const bool flagged = q.pinned_ids[0] || q.pinned_ids[1] >= 0;
+        const int at = flagged ? q.pinned_ids[3] : step;  // the step that set the flags
+        g_decode_steps = at + 1;
         if (q.pinned_ids[2]) return fail(WH_ERR_HIP, "model: decode: beam search: candidate sort stack exhausted");
         if (q.pinned_ids[0]) break;
-        if (q.pinned_ids[1] >= 0 && step + 1 < mt)
+        if (q.pinned_ids[1] >= 0 && at + 1 < mt)
             return fail(WH_ERR_INVALID, "model: decode: beam search forward: model: decode: forward: position " +
                                             std::to_string(q.pinned_ids[1]) + " >= context length " +
                                             std::to_string(m->n_ctx));
+        if (q.pinned_ids[1] >= 0) break;
     }
     int32_t o0 = 0, len0 = 0;
     WH_HIP(hipMemcpy(&o0, order, sizeof(int32_t), hipMemcpyDeviceToHost));
