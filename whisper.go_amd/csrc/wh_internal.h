@@ -143,13 +143,14 @@ int launch_self_attn(const float *q, const float *k, const float *v, float *kv_l
 struct CrossBufs {
     float *scores;     // [S][H][enc_len]
     float *cmax;       // [S][H][C]
-    float *psum;       // [S][H][C]
-    float *pv;         // [S][H][C][hd]
+    uint64_t *pvt;     // [S][H][C][65] {launch number, value}: a chunk's weights . V and its weight sum
+    uint32_t *cnt;     // [S][H] chunks arrived, zero between launches
+    uint32_t seq;      // launch number of the last head-size-64 launch
     int chunks;
     int chunk_len;
 };
 int launch_cross_attn(const float *q, const float *const *kbase, const float *const *vbase, const int32_t *active,
-                      float *out, int S, int H, int hd, int enc_len, const CrossBufs &b, hipStream_t st);
+                      float *out, int S, int H, int hd, int enc_len, CrossBufs &b, hipStream_t st);
 // out[T, rows] = enc[T, cols] . w^T (+ bias); gelu: gelu of that; res: res + that.
 int launch_cross_gemm(const DevMat &w, const float *enc, int enc_len, const float *bias, float *out,
                       hipStream_t st, int gelu = 0, const float *res = nullptr);

@@ -708,20 +708,29 @@ __global__ __launch_bounds__(64 * NW) void k_gemv_mfma(GemvArgs a) {
         __syncthreads();
         if (!last) return;
         if (tid < 256) {
+            // all the other splits' pairs are loaded at once, then any pair not yet
+            // carrying this launch's number is read again
+            uint64_t pr[GEMVM_MAX_SPLIT];
+#pragma unroll
+            for (int j = 0; j < GEMVM_MAX_SPLIT; j++)
+                if (j < nsplit && j != split)
+                    pr[j] = __hip_atomic_load(pt + j * 256 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             float sum = 0.0f;
-            for (int j = 0; j < nsplit; j++) {
+#pragma unroll
+            for (int j = 0; j < GEMVM_MAX_SPLIT; j++) {
+                if (j >= nsplit) break;
                 float pj = v;
                 if (j != split) {
-                    uint64_t pr = __hip_atomic_load(pt + j * 256 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    for (int spin = 0; (pr & 0xffffffff00000000ull) != tag; spin++) {
+                    uint64_t q = pr[j];
+                    for (int spin = 0; (q & 0xffffffff00000000ull) != tag; spin++) {
                         if (spin >= (1 << 20)) {
-                            pr = tag | 0x7fc00000u;  // NaN
+                            q = tag | 0x7fc00000u;  // NaN
                             break;
                         }
                         __builtin_amdgcn_s_sleep(1);
-                        pr = __hip_atomic_load(pt + j * 256 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        q = __hip_atomic_load(pt + j * 256 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
-                    pj = __uint_as_float((uint32_t)pr);
+                    pj = __uint_as_float((uint32_t)q);
                 }
                 sum += pj;
             }
@@ -1271,11 +1280,13 @@ int launch_self_attn(const float *q, const float *k, const float *v, float *kv_l
 // (internal/model/decoder.go:911-971, P3 addressing :949-951): the [enc_len, d]
 // row-major projection is viewed as [H, enc_len, hd] without a transpose, so
 // head h reads the contiguous slab [h*enc_len*hd, (h+1)*enc_len*hd).
-// hd == 64: split over key chunks in three kernels; the softmax subtracts the
-// exact global maximum before the fast exp, as the reference does
-// (attention.go:93-131). Other head sizes: one block per (stream, head).
+// hd == 64: split over key chunks in two kernels (the last chunk of a head
+// combines it); the softmax subtracts the exact global maximum before the fast
+// exp, as the reference does (attention.go:93-131). Other head sizes: one block
+// per (stream, head).
 // ---------------------------------------------------------------------------
 constexpr int CROSS_CHUNK = 128;
+constexpr int CROSS_MAXC = 16;  // key chunks per head (encoder lengths up to 2048)
 
 __global__ __launch_bounds__(256) void k_cross_scores64(const float *q, const float *const *kbase,
                                                         const int32_t *active, float *scores, float *cmax, int H,
@@ -1316,11 +1327,21 @@ __global__ __launch_bounds__(256) void k_cross_scores64(const float *q, const fl
     if (threadIdx.x == 0) cmax[((size_t)s * H + h) * chunks + c] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
+// Weights . V of one chunk; the chunk workgroup that arrives last for its
+// (stream, head) then combines the head: the chunks' weight sums and partial
+// products summed in chunk order, times the reciprocal of the sum. The partials
+// travel as {launch number, value} pairs stored and read at agent scope (no
+// fences: on this chip they write back or drop the whole L2); the last workgroup
+// reads each pair until it carries this launch's number (a counted chunk's pairs
+// are in flight, so the bounded wait ends at once; one that never arrives gives
+// NaN). The counter goes back to zero.
 __global__ __launch_bounds__(256) void k_cross_pv64(const float *const *vbase, const int32_t *active,
-                                                    const float *scores, const float *cmax, float *psum, float *pv,
-                                                    int H, int enc_len, int chunks) {
+                                                    const float *scores, const float *cmax, uint64_t *pvt,
+                                                    uint32_t *cnt, uint32_t seq, float *out, int H, int enc_len,
+                                                    int chunks) {
     __shared__ float4 red4[4][16];
     __shared__ float reds[4];
+    __shared__ int last;
     const int c = blockIdx.x % chunks, sh = blockIdx.x / chunks, h = sh % H, s = sh / H;
     if (active && !active[s]) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, slot = lane & 15;
@@ -1364,28 +1385,56 @@ __global__ __launch_bounds__(256) void k_cross_pv64(const float *const *vbase, c
     if (lane < 16) red4[wave][lane] = acc;
     if (lane == 0) reds[wave] = es;
     __syncthreads();
+    const uint64_t tag = (uint64_t)seq << 32;
+    uint64_t *pt = pvt + (size_t)sh * chunks * 65;
     if (threadIdx.x < 16) {
         float4 r = red4[0][threadIdx.x];
         for (int w = 1; w < 4; w++) {
             float4 t = red4[w][threadIdx.x];
             r.x += t.x; r.y += t.y; r.z += t.z; r.w += t.w;
         }
-        ((float4 *)(pv + (((size_t)s * H + h) * chunks + c) * 64))[threadIdx.x] = r;
+        uint64_t *p = pt + (size_t)c * 65 + 4 * threadIdx.x;
+        __hip_atomic_store(p, tag | __float_as_uint(r.x), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p + 1, tag | __float_as_uint(r.y), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p + 2, tag | __float_as_uint(r.z), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p + 3, tag | __float_as_uint(r.w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (threadIdx.x == 0) psum[((size_t)s * H + h) * chunks + c] = (reds[0] + reds[1]) + (reds[2] + reds[3]);
-}
-
-__global__ __launch_bounds__(64) void k_cross_combine64(const int32_t *active, const float *psum, const float *pv,
-                                                        float *out, int H, int chunks) {
-    const int sh = blockIdx.x, h = sh % H, s = sh / H;
-    if (active && !active[s]) return;
-    const float *ps = psum + (size_t)sh * chunks;
-    float sum = 0.0f;
-    for (int i = 0; i < chunks; i++) sum += ps[i];
+    if (threadIdx.x == 16)
+        __hip_atomic_store(pt + (size_t)c * 65 + 64, tag | __float_as_uint((reds[0] + reds[1]) + (reds[2] + reds[3])),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(cnt + sh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(chunks - 1);
+    __syncthreads();
+    if (!last || threadIdx.x >= 64) return;
+    // every chunk's pairs are loaded at once; a pair not yet carrying this
+    // launch's number is read again
+    const int j = threadIdx.x;
+    uint64_t ps[CROSS_MAXC], pj[CROSS_MAXC];
+#pragma unroll
+    for (int i = 0; i < CROSS_MAXC; i++)
+        if (i < chunks) {
+            ps[i] = __hip_atomic_load(pt + (size_t)i * 65 + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            pj[i] = __hip_atomic_load(pt + (size_t)i * 65 + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    auto settle = [&](uint64_t v, const uint64_t *p) {
+        for (int spin = 0; (v & 0xffffffff00000000ull) != tag; spin++) {
+            if (spin >= (1 << 20)) return __uint_as_float(0x7fc00000u);  // NaN
+            __builtin_amdgcn_s_sleep(1);
+            v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return __uint_as_float((uint32_t)v);
+    };
+    float sum = 0.0f, o = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CROSS_MAXC; i++)
+        if (i < chunks) sum += settle(ps[i], pt + (size_t)i * 65 + 64);
     const float inv = 1.0f / sum;  // sum >= 1: the maximum key contributes fast_exp(0) = 1
-    float o = 0.0f;
-    for (int i = 0; i < chunks; i++) o += pv[((size_t)sh * chunks + i) * 64 + threadIdx.x];
-    out[(size_t)s * H * 64 + h * 64 + threadIdx.x] = o * inv;
+#pragma unroll
+    for (int i = 0; i < CROSS_MAXC; i++)
+        if (i < chunks) o += settle(pj[i], pt + (size_t)i * 65 + j);
+    out[(size_t)s * H * 64 + h * 64 + j] = o * inv;
+    if (j == 0) __hip_atomic_store(cnt + sh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __global__ __launch_bounds__(256) void k_cross_generic(const float *q, const float *const *kbase,
@@ -1431,15 +1480,15 @@ __global__ __launch_bounds__(256) void k_cross_generic(const float *q, const flo
 }
 
 int launch_cross_attn(const float *q, const float *const *kbase, const float *const *vbase, const int32_t *active,
-                      float *out, int S, int H, int hd, int enc_len, const CrossBufs &b, hipStream_t st) {
+                      float *out, int S, int H, int hd, int enc_len, CrossBufs &b, hipStream_t st) {
     float scale = (float)(1.0 / sqrt((double)hd));
-    if (hd == 64) {
+    if (hd == 64 && b.chunks <= CROSS_MAXC) {
         int chunks = b.chunks;
+        if (++b.seq == 0) ++b.seq;  // 0 is the tag of the zeroed buffer
         hipLaunchKernelGGL(k_cross_scores64, dim3(S * H * chunks), dim3(256), 0, st, q, kbase, active, b.scores,
                            b.cmax, H, enc_len, chunks, scale);
         hipLaunchKernelGGL(k_cross_pv64, dim3(S * H * chunks), dim3(256), 0, st, vbase, active, b.scores, b.cmax,
-                           b.psum, b.pv, H, enc_len, chunks);
-        hipLaunchKernelGGL(k_cross_combine64, dim3(S * H), dim3(64), 0, st, active, b.psum, b.pv, out, H, chunks);
+                           b.pvt, b.cnt, b.seq, out, H, enc_len, chunks);
     } else {
         size_t shmem = sizeof(float) * (size_t)enc_len;
         if (shmem > 64 * 1024) return fail(WH_ERR_UNSUPPORTED, "cross-attention: encoder length too large for head size");

@@ -676,8 +676,10 @@ int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t e
     s->cb.chunks = (enc_len + 127) / 128;
     ALLOC(s->cb.scores, (size_t)S * H * enc_len);
     ALLOC(s->cb.cmax, (size_t)S * H * s->cb.chunks);
-    ALLOC(s->cb.psum, (size_t)S * H * s->cb.chunks);
-    ALLOC(s->cb.pv, (size_t)S * H * s->cb.chunks * 64);
+    ALLOC(s->cb.pvt, (size_t)S * H * s->cb.chunks * 65);
+    ALLOC(s->cb.cnt, (size_t)S * H);
+    WH_HIP(hipMemsetAsync(s->cb.pvt, 0, sizeof(uint64_t) * S * H * s->cb.chunks * 65, s->st));
+    WH_HIP(hipMemsetAsync(s->cb.cnt, 0, sizeof(uint32_t) * S * H, s->st));
     s->sb.parts = SAMPLE_PARTS;
     ALLOC(s->sb.cur, (size_t)S * V);
     ALLOC(s->sb.part_val, (size_t)S * SAMPLE_PARTS);
