@@ -267,9 +267,13 @@ int forward(const wh_encoder *e, const Work &w, const float *mel, int T, float *
         const wh_encoder::Block &b = e->blocks[i];
         // self-attention sub-layer (encoder.go:310-317, 340-379)
         if ((rc = launch_layernorm(w.x, b.ln1w, b.ln1b, w.xln, tp, d, st))) return rc;
-        if ((rc = launch_cross_gemm(b.q, w.xln, tp, b.qb, w.q, st))) return rc;
-        if ((rc = launch_cross_gemm(b.k, w.xln, tp, nullptr, w.k, st))) return rc;
-        if ((rc = launch_cross_gemm(b.v, w.xln, tp, b.vb, w.v, st))) return rc;
+        {
+            // q, k and v of the same rows in one launch
+            const DevMat *qkv[3] = {&b.q, &b.k, &b.v};
+            const float *qkvb[3] = {b.qb, nullptr, b.vb};
+            float *qkvo[3] = {w.q, w.k, w.v};
+            if ((rc = launch_cross_gemm_n(qkv, 3, w.xln, tp, qkvb, qkvo, st))) return rc;
+        }
         if ((rc = launch_enc_attn(w.q, w.k, w.v, tp, d, H, w.att, st))) return rc;
         if ((rc = launch_cross_gemm(b.o, w.att, tp, b.ob, w.x, st, 0, w.x))) return rc;
         // MLP sub-layer (encoder.go:319-325, 383-396)

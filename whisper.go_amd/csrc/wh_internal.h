@@ -154,6 +154,10 @@ int launch_cross_attn(const float *q, const float *const *kbase, const float *co
 // out[T, rows] = enc[T, cols] . w^T (+ bias); gelu: gelu of that; res: res + that.
 int launch_cross_gemm(const DevMat &w, const float *enc, int enc_len, const float *bias, float *out,
                       hipStream_t st, int gelu = 0, const float *res = nullptr);
+// The same for n (1..3) matrices over the same frames in one launch when they
+// share type and row length (otherwise one launch each): out[i] = enc . ws[i]^T + bias[i].
+int launch_cross_gemm_n(const DevMat *const *ws, int n, const float *enc, int enc_len, const float *const *bias,
+                        float *const *out, hipStream_t st, int gelu = 0, const float *res = nullptr);
 // encoder kernels (wh_encoder.hip)
 int launch_im2col(const float *in, int64_t sc, int64_t st, int cin, int tin, int stride, int tout, int K, float *out,
                   hipStream_t s);

@@ -1583,13 +1583,30 @@ __device__ __forceinline__ void dequant8(const MatView &m, int r, int b, int g, 
 // Epilogue: v = acc + bias; gelu: C = gelu(v); res: C = res + v (res may alias C).
 // BK blocks of 32 columns per K-step (one LDS stage and two barriers per step);
 // a row's last step with fewer blocks left stages zeros in their place.
+// Up to three products of the same frames in one launch (grid z), e.g. the cross
+// K and V of a layer or the encoder's q, k and v; res and gelu apply to every one.
+struct XGemmOps {
+    MatView w[3];
+    const float *bias[3];
+    float *C[3];
+    const float *res;
+    int gelu;
+};
+
 template <int TYPE, int BK>
-__global__ __launch_bounds__(256) void k_cross_gemm(MatView w, const float *E, int T, const float *bias, float *C,
-                                                    int gelu, const float *res) {
+__global__ __launch_bounds__(256) void k_cross_gemm(XGemmOps ops, const float *E, int T) {
     constexpr int KW = 32 * BK, KP = KW + 1;  // columns per step; LDS row stride (conflict-free operand reads)
     __shared__ float Es[64][KP];  // [frame][k]
     __shared__ float Ws[64][KP];  // [row][k]
+    // this workgroup's matrix: grid z picks one of ops.n products of the same frames
+    const int z = blockIdx.z;
+    const MatView w = z == 0 ? ops.w[0] : z == 1 ? ops.w[1] : ops.w[2];
+    const float *bias = z == 0 ? ops.bias[0] : z == 1 ? ops.bias[1] : ops.bias[2];
+    float *C = z == 0 ? ops.C[0] : z == 1 ? ops.C[1] : ops.C[2];
+    const int gelu = ops.gelu;
+    const float *res = ops.res;
     const int t0 = blockIdx.y * 64, r0 = blockIdx.x * 64;
+    if (r0 >= w.rows) return;  // the whole workgroup: past this matrix's rows
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int wt = (wave >> 1) * 32, wr = (wave & 1) * 32;  // this wave's quarter of the tile
     const int K = w.cols;
@@ -1715,35 +1732,61 @@ __global__ __launch_bounds__(256) void k_cross_gemm_simt(MatView w, const float 
     }
 }
 
-int launch_cross_gemm(const DevMat &w, const float *enc, int enc_len, const float *bias, float *out, hipStream_t st,
-                      int gelu, const float *res) {
-    MatView v = view_of(w);
-    dim3 grid((w.rows + 63) / 64, (enc_len + 63) / 64);
-    if (w.cols % 32 != 0 || (((uintptr_t)enc) & 15) != 0) {
-        // a partial last block or unaligned frame rows: the vector-unit GEMM
-        switch (w.type) {
-        case 0: hipLaunchKernelGGL(k_cross_gemm_simt<0>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
-        case 2: hipLaunchKernelGGL(k_cross_gemm_simt<2>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
-        case 3: hipLaunchKernelGGL(k_cross_gemm_simt<3>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
-        case 6: hipLaunchKernelGGL(k_cross_gemm_simt<6>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
-        case 7: hipLaunchKernelGGL(k_cross_gemm_simt<7>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
-        case 8: hipLaunchKernelGGL(k_cross_gemm_simt<8>, grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
-        default: return fail(WH_ERR_UNSUPPORTED, "cross gemm: unsupported type");
+int launch_cross_gemm_n(const DevMat *const *ws, int n, const float *enc, int enc_len, const float *const *bias,
+                        float *const *out, hipStream_t st, int gelu, const float *res) {
+    if (n < 1 || n > 3) return fail(WH_ERR_INVALID, "cross gemm: 1..3 matrices per launch");
+    bool same = true;
+    for (int i = 1; i < n; i++) same &= ws[i]->type == ws[0]->type && ws[i]->cols == ws[0]->cols;
+    if (!same || ws[0]->cols % 32 != 0 || (((uintptr_t)enc) & 15) != 0) {
+        // mixed matrices, a partial last block or unaligned frame rows: one
+        // vector-unit GEMM per matrix
+        for (int i = 0; i < n; i++) {
+            const DevMat &w = *ws[i];
+            MatView v = view_of(w);
+            dim3 grid((w.rows + 63) / 64, (enc_len + 63) / 64);
+            const float *b = bias[i];
+            float *o = out[i];
+            switch (w.type) {
+            case 0: hipLaunchKernelGGL(k_cross_gemm_simt<0>, grid, dim3(256), 0, st, v, enc, enc_len, b, o, gelu, res); break;
+            case 2: hipLaunchKernelGGL(k_cross_gemm_simt<2>, grid, dim3(256), 0, st, v, enc, enc_len, b, o, gelu, res); break;
+            case 3: hipLaunchKernelGGL(k_cross_gemm_simt<3>, grid, dim3(256), 0, st, v, enc, enc_len, b, o, gelu, res); break;
+            case 6: hipLaunchKernelGGL(k_cross_gemm_simt<6>, grid, dim3(256), 0, st, v, enc, enc_len, b, o, gelu, res); break;
+            case 7: hipLaunchKernelGGL(k_cross_gemm_simt<7>, grid, dim3(256), 0, st, v, enc, enc_len, b, o, gelu, res); break;
+            case 8: hipLaunchKernelGGL(k_cross_gemm_simt<8>, grid, dim3(256), 0, st, v, enc, enc_len, b, o, gelu, res); break;
+            default: return fail(WH_ERR_UNSUPPORTED, "cross gemm: unsupported type");
+            }
+            WH_HIP(hipGetLastError());
         }
-        WH_HIP(hipGetLastError());
         return WH_OK;
     }
-    switch (w.type) {
-    case 0: hipLaunchKernelGGL((k_cross_gemm<0, 2>), grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
-    case 2: hipLaunchKernelGGL((k_cross_gemm<2, 2>), grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
-    case 3: hipLaunchKernelGGL((k_cross_gemm<3, 2>), grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
-    case 6: hipLaunchKernelGGL((k_cross_gemm<6, 2>), grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
-    case 7: hipLaunchKernelGGL((k_cross_gemm<7, 2>), grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
-    case 8: hipLaunchKernelGGL((k_cross_gemm<8, 2>), grid, dim3(256), 0, st, v, enc, enc_len, bias, out, gelu, res); break;
+    XGemmOps ops{};
+    int rows = 0;
+    for (int i = 0; i < n; i++) {
+        ops.w[i] = view_of(*ws[i]);
+        ops.bias[i] = bias[i];
+        ops.C[i] = out[i];
+        rows = std::max(rows, ws[i]->rows);
+    }
+    ops.res = res;
+    ops.gelu = gelu;
+    dim3 grid((rows + 63) / 64, (enc_len + 63) / 64, n);
+    switch (ws[0]->type) {
+    case 0: hipLaunchKernelGGL((k_cross_gemm<0, 2>), grid, dim3(256), 0, st, ops, enc, enc_len); break;
+    case 2: hipLaunchKernelGGL((k_cross_gemm<2, 2>), grid, dim3(256), 0, st, ops, enc, enc_len); break;
+    case 3: hipLaunchKernelGGL((k_cross_gemm<3, 2>), grid, dim3(256), 0, st, ops, enc, enc_len); break;
+    case 6: hipLaunchKernelGGL((k_cross_gemm<6, 2>), grid, dim3(256), 0, st, ops, enc, enc_len); break;
+    case 7: hipLaunchKernelGGL((k_cross_gemm<7, 2>), grid, dim3(256), 0, st, ops, enc, enc_len); break;
+    case 8: hipLaunchKernelGGL((k_cross_gemm<8, 2>), grid, dim3(256), 0, st, ops, enc, enc_len); break;
     default: return fail(WH_ERR_UNSUPPORTED, "cross gemm: unsupported type");
     }
     WH_HIP(hipGetLastError());
     return WH_OK;
+}
+
+int launch_cross_gemm(const DevMat &w, const float *enc, int enc_len, const float *bias, float *out, hipStream_t st,
+                      int gelu, const float *res) {
+    const DevMat *ws[1] = {&w};
+    return launch_cross_gemm_n(ws, 1, enc, enc_len, &bias, &out, st, gelu, res);
 }
 
 // ---------------------------------------------------------------------------

@@ -742,8 +742,11 @@ int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t e
             const Layer &l = m->layers[li];
             float *K = s->crossK + ((size_t)e * L + li) * enc_len * d;
             float *Vv = s->crossV + ((size_t)e * L + li) * enc_len * d;
-            if ((rc = launch_cross_gemm(l.ck, enc, enc_len, nullptr, K, s->st)) ||
-                (rc = launch_cross_gemm(l.cv, enc, enc_len, l.cvb, Vv, s->st))) {
+            // the layer's K and V in one launch
+            const DevMat *kv[2] = {&l.ck, &l.cv};
+            const float *kvb[2] = {nullptr, l.cvb};
+            float *kvo[2] = {K, Vv};
+            if ((rc = launch_cross_gemm_n(kv, 2, enc, enc_len, kvb, kvo, s->st))) {
                 (void)hipStreamSynchronize(s->st);
                 (void)hipFree(stage);
                 return rc;
