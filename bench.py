@@ -58,7 +58,7 @@ def cpu_model():
 
 
 def host_cores():
-    """CPUs this process may run on (the box's share, not the machine's count)."""
+    """CPUs this process may run on (its affinity share, not the machine's count)."""
     try:
         return len(os.sched_getaffinity(0))
     except AttributeError:
@@ -72,7 +72,7 @@ def prefix_match(a, b):
 
 
 def cpu_baseline(wh, tensors, meta, enc, prompt, n_tokens, gpu_tokens):
-    from oracle import oracle as orc  # the checker, timed as the CPU baseline
+    from oracle import oracle as orc  # the oracle, timed as the CPU baseline
 
     threads = min(16, host_cores())
     t0 = time.time()
@@ -365,7 +365,7 @@ def run_encoder(args):
     dout.free()
     enc.close()
     if args.cpu_tokens > 0:
-        from oracle import oracle as orc  # the checker, timed as the CPU baseline
+        from oracle import oracle as orc  # the oracle, timed as the CPU baseline
 
         threads = min(16, host_cores())
         n_blk = 1
@@ -528,7 +528,7 @@ def main():
                          "(for kernel-trace profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench: this build runs on one GPU; --gpus {args.gpus} is not supported "
+        print(f"bench: the benchmark runs on one GPU; --gpus {args.gpus} is not supported "
               "(streams shard data-parallel across GPUs with no collective)", file=sys.stderr)
         sys.exit(2)
     if args.gemv:

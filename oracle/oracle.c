@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the whisper.go decoder token loop — TEST INFRASTRUCTURE ONLY.
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it,
- * as the checker. Restates the reference (github.com/whispergo/whisper.go);
+ * to check and time against. Restates the reference (github.com/whispergo/whisper.go);
  * every function cites the file:line it follows. See oracle.h for what pins
  * each part and what stays "parity unpinned".
  *

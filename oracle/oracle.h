@@ -3,8 +3,9 @@
  *
  * TEST INFRASTRUCTURE ONLY. This is a plain-C restatement of the reference
  * algorithm (wxcdart/whisper.go, Go module github.com/whispergo/whisper.go),
- * used by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg as
- * the checker. The product (libwhisper_hip.so) never links, loads or calls it.
+ * used by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg to
+ * check and time against. The product (libwhisper_hip.so) never links, loads or
+ * calls it.
  *
  * Each function cites the reference file:line it restates. Float arithmetic
  * is float32 with no FMA contraction (Go on amd64, GOAMD64=v1, does not fuse),

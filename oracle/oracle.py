@@ -1,7 +1,7 @@
 """ctypes wrapper of the CPU oracle (oracle/_build/liboracle.so).
 
 TEST INFRASTRUCTURE ONLY: used by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py as the checker. See oracle.h for the reference
+cpu_baseline leg of bench.py to check and time against. See oracle.h for the reference
 file:line each function restates and for what pins it.
 """
 import ctypes as C

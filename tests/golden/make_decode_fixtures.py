@@ -1,4 +1,4 @@
-"""Writes the oracle's decode results for the survey's workloads as fixtures.
+"""Writes the oracle's decode results for the full-size decode workloads as fixtures.
 
 For each workload the synthetic model and encoder outputs are regenerated from
 their seeds (whisper.go_amd/synth.py), so the fixture holds only results:

@@ -1,4 +1,4 @@
-"""The survey's full-size workloads on the device against the oracle's results.
+"""The full-size decode workloads on the device against the oracle's results.
 
 The oracle's token sequences, per-step margins and first-step logits are
 committed fixtures (tests/golden/make_decode_fixtures.py writes them on the
