@@ -195,15 +195,19 @@ def test_batch_equals_single_streams(wh, orc, gpu):
         assert got[i] == ref.decode(encs[i], params[i]), i
 
 
-@pytest.mark.parametrize("qtype", [3, 8, 2, 6, 7])
-def test_sixteen_streams_split_gemv_vs_oracle(wh, orc, gpu, qtype):
+@pytest.mark.parametrize("qtype,dims", [(3, (1000, 512, 8, 2, 64)), (8, (1000, 512, 8, 2, 64)),
+                                        (2, (1000, 512, 8, 2, 64)), (6, (1000, 512, 8, 2, 64)),
+                                        (7, (1000, 512, 8, 2, 64)), (3, (1000, 768, 12, 1, 64))])
+def test_sixteen_streams_split_gemv_vs_oracle(wh, orc, gpu, qtype, dims):
     """16 streams on the multi-kernel chain: the matrix-core GEMV at batch 16 with
-    K split over several workgroups per 16-row tile (2 ranges of the 512-column
-    rows, 4 of the 2048-column fc2 rows), the last workgroup of a tile summing the
-    partial tiles; every stream's logits at every step against the oracle."""
-    name = f"s16split{qtype}"
-    tensors, meta = _model(wh, name, qtype, (1000, 512, 8, 2, 64))
-    encs = [wh.synth.encoder_output(name, 512, stream=i, enc_len=48) for i in range(16)]
+    K split over several workgroups per 16-row tile (d = 512: 2 ranges of the
+    512-column rows, 4 of the 2048-column fc2 rows; d = 768: fc1's 3072 rows take
+    the taller matrices' kernel, 3 ranges), the last workgroup of a tile summing
+    the partial tiles; every stream's logits at every step against the oracle."""
+    d = dims[1]
+    name = f"s16split{qtype}_{d}"
+    tensors, meta = _model(wh, name, qtype, dims)
+    encs = [wh.synth.encoder_output(name, d, stream=i, enc_len=48) for i in range(16)]
     dec = wh.HIPDecoder(tensors, meta)
     ref = orc.OracleModel(tensors, meta)
     seq = dec.sequence(encs)

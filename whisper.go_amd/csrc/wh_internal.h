@@ -119,6 +119,9 @@ struct GemvIn {
 // pairs (zero when allocated) and one arrival counter per tile (zero when
 // allocated; the kernel leaves it zero). `seq` numbers the launches.
 constexpr int GEMVM_MAX_SPLIT = 4;
+#ifndef GEMVM_SPLIT_TILES
+#define GEMVM_SPLIT_TILES 320  // row tiles a sequence's workspace holds
+#endif
 struct GemvWork {
     uint64_t *part = nullptr;  // tiles * GEMVM_MAX_SPLIT * 256 pairs
     uint32_t *cnt = nullptr;   // tiles counters

@@ -550,6 +550,9 @@ __global__ __launch_bounds__(256) void k_gemv2(GemvArgs a, int ch) {
 #ifndef GEMVM_NW_TALL
 #define GEMVM_NW_TALL 10
 #endif
+#ifndef GEMVM_WG_TARGET_TALL
+#define GEMVM_WG_TARGET_TALL 640  // the same for taller matrices (three 42 KiB workgroups fit a CU)
+#endif
 #ifndef GEMVM_WG_TARGET
 #define GEMVM_WG_TARGET 256  // split K up to this many workgroups
 #endif
@@ -771,8 +774,8 @@ static bool gemvm_launch(GemvArgs &a, int maxrows, GemvWork *work, hipStream_t s
     int tiles = 0;
     for (int i = 0; i < a.nop; i++) tiles += (a.op[i].rows + 15) / 16;
     a.nsplit = 1;
-    if (work && work->part && maxrows <= GEMVM_SMALL_ROWS && tiles <= work->tiles) {
-        int nsplit = GEMVM_WG_TARGET / tiles;
+    if (work && work->part && tiles <= work->tiles) {
+        int nsplit = (maxrows <= GEMVM_SMALL_ROWS ? GEMVM_WG_TARGET : GEMVM_WG_TARGET_TALL) / tiles;
         int nbmin = a.op[0].nb;
         for (int i = 1; i < a.nop; i++) nbmin = std::min(nbmin, a.op[i].nb);
         nsplit = std::min(std::min(nsplit, GEMVM_MAX_SPLIT), std::max(1, nbmin / 8));

@@ -700,8 +700,8 @@ int seq_create(const wh_model *m, int32_t S, const float *const *encs, int32_t e
     ALLOC(s->topk_logz, (size_t)S);
     ALLOC(s->topk_part, (size_t)TOPK_SCRATCH_FLOATS);
     if (S >= 6) {
-        // split-K workspace of the batched GEMV: up to 128 row tiles are split
-        s->gw.tiles = 128;
+        // split-K workspace of the batched GEMV
+        s->gw.tiles = GEMVM_SPLIT_TILES;
         ALLOC(s->gw.part, (size_t)s->gw.tiles * GEMVM_MAX_SPLIT * 256);
         ALLOC(s->gw.cnt, (size_t)s->gw.tiles);
         WH_HIP(hipMemsetAsync(s->gw.part, 0, sizeof(uint64_t) * s->gw.tiles * GEMVM_MAX_SPLIT * 256, s->st));
