@@ -1195,6 +1195,17 @@ __global__ __launch_bounds__(NT) void k_fwd_batch(BArgs a) {
     if (threadIdx.x == 0) __hip_atomic_store(flags + w, g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Loads the code objects of the instantiations a model of width d launches (the
+// runtime loads them on first use otherwise, in the first step).
+template <int TYPE>
+int warm_type(int d) {
+    hipFuncAttributes attr;
+    const void *fns[2] = {d <= 1024 ? (const void *)k_fwd_batch<TYPE, 32, false> : (const void *)k_fwd_batch<TYPE, 64, false>,
+                          d <= 1024 ? (const void *)k_fwd_batch<TYPE, 32, true> : (const void *)k_fwd_batch<TYPE, 64, true>};
+    for (const void *fn : fns) WH_HIP(hipFuncGetAttributes(&attr, fn));
+    return WH_OK;
+}
+
 // Launch of the kernel for weight type TYPE; G from the model width.
 template <int TYPE>
 int launch_type(int grid, const BArgs &a, hipStream_t st) {

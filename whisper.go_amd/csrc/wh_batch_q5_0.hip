@@ -4,5 +4,6 @@
 namespace wh {
 namespace batch {
 int launch_q5_0(int grid, const BArgs &a, hipStream_t st) { return launch_type<6>(grid, a, st); }
+int warm_q5_0(int d) { return warm_type<6>(d); }
 }  // namespace batch
 }  // namespace wh

@@ -14,6 +14,15 @@
 #include "wh_load.h"
 
 namespace wh {
+namespace mega {
+int warm_decode(uint32_t type);
+}
+namespace batch {
+int warm(uint32_t type, int d);
+}
+}  // namespace wh
+
+namespace wh {
 
 namespace {
 
@@ -360,6 +369,8 @@ int model_create(const wh_tensor *tensors, int32_t n, const wh_meta *meta, int32
         for (const DevMat *x : ms) wb += x->algo_bytes;
     }
     m->weight_bytes = wb;
+    // load the persistent kernels' code objects now rather than in the first step
+    if ((rc = mega::warm_decode(m->tok.type)) || (rc = batch::warm(m->tok.type, d))) return rc;
     *out = m.release();
     return WH_OK;
 }
