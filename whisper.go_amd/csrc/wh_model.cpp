@@ -371,6 +371,13 @@ int model_create(const wh_tensor *tensors, int32_t n, const wh_meta *meta, int32
     m->weight_bytes = wb;
     // load the persistent kernels' code objects now rather than in the first step
     if ((rc = mega::warm_decode(m->tok.type)) || (rc = batch::warm(m->tok.type, d))) return rc;
+    {
+        // the runtime sets up a stream's hardware queue on first use (~3 ms of the
+        // first sequence's setup otherwise); it keeps it for the next stream
+        hipStream_t st = nullptr;
+        WH_HIP(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+        WH_HIP(hipStreamDestroy(st));
+    }
     *out = m.release();
     return WH_OK;
 }
