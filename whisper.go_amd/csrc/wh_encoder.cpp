@@ -202,6 +202,10 @@ int encoder_create(const wh_tensor *tensors, int32_t n, const wh_enc_meta *meta,
     WH_HIP(hipMalloc(&e->vec_alloc, arena.host.size() * sizeof(float) + 256));
     WH_HIP(hipMemcpy(e->vec_alloc, arena.host.data(), arena.host.size() * sizeof(float), hipMemcpyHostToDevice));
     for (auto &f : arena.fix) *f.first = (float *)e->vec_alloc + f.second;
+    // the forward's stream and code objects now, not in the first encode (the
+    // runtime sets up a stream's hardware queue and loads code on first use)
+    WH_HIP(hipStreamCreateWithFlags(&e->st, hipStreamNonBlocking));
+    if ((rc = warm_encoder_kernels()) || (rc = warm_kernels())) return rc;
     *out = e.release();
     return WH_OK;
 }

@@ -300,6 +300,13 @@ int launch_gelu_add(float *x, const float *pos, int64_t n, hipStream_t s) {
     return WH_OK;
 }
 
+// Loads this file's code object (the runtime does it on first use otherwise).
+int warm_encoder_kernels() {
+    hipFuncAttributes attr;
+    WH_HIP(hipFuncGetAttributes(&attr, (const void *)k_enc_attn_mfma<4, 2>));
+    return WH_OK;
+}
+
 int launch_enc_attn(const float *Q, const float *K, const float *V, int T, int d, int H, float *out, hipStream_t s) {
     const int hd = d / H;
     const float scale = (float)(1.0 / sqrt((double)hd));

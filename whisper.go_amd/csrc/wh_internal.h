@@ -166,6 +166,9 @@ int launch_im2col(const float *in, int64_t sc, int64_t st, int cin, int tin, int
                   hipStream_t s);
 int launch_gelu_add(float *x, const float *pos, int64_t n, hipStream_t s);
 int launch_enc_attn(const float *Q, const float *K, const float *V, int T, int d, int H, float *out, hipStream_t s);
+// Load the code objects of wh_encoder.hip and wh_kernels.hip ahead of their first launch.
+int warm_encoder_kernels();
+int warm_kernels();
 struct SampleBufs {
     float *cur;          // [S][V] penalised logits
     float *part_val;     // [S][P]

@@ -1105,6 +1105,13 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *x, const float *
     for (int i = threadIdx.x; i < d; i += blockDim.x) yr[i] = w[i] * (xr[i] - mean) / sd + b[i];
 }
 
+// Loads this file's code object (the runtime does it on first use otherwise).
+int warm_kernels() {
+    hipFuncAttributes attr;
+    WH_HIP(hipFuncGetAttributes(&attr, (const void *)k_layernorm));
+    return WH_OK;
+}
+
 int launch_layernorm(const float *x, const float *w, const float *b, float *y, int S, int d, hipStream_t st) {
     hipLaunchKernelGGL(k_layernorm, dim3(S), dim3(256), 0, st, x, w, b, y, d);
     WH_HIP(hipGetLastError());
